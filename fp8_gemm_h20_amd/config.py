@@ -1,0 +1,181 @@
+"""CPU-only profile loading, schema validation and deterministic M -> entry selection.
+
+Same public functions and behaviour as the reference's fp8_gemm_h20/config.py:
+available_profiles, token_tile, validate_config, get_profile, supports, select
+(config.py:13-105, policy prose in docs/configuration.md:26-38).  No torch,
+no GPU: only json/math/copy/functools.
+
+Differences, all additive:
+* Packaged tables (configs/*.json) are gfx950 tables whose entries use the
+  native impls "xdl"/"shortk".  Their tile rule is widened: BLOCK_W in
+  {64, 128, 256} (a 256-row tile spans two 128-row weight-scale blocks) and
+  BLOCK_T a power of two in 16..256.  Entries with the reference's impl
+  names keep the reference's rule (BLOCK_W divides 128, power-of-two token
+  tile), so the reference's own H20 tables validate and route unchanged.
+* `select_in(data, M, N, K)` / `supports_in(...)` apply the policy to any
+  validated table dict, e.g. a table loaded with `load_profile(path)`.
+"""
+import copy
+import json
+import math
+from functools import lru_cache
+from pathlib import Path
+
+from .engine import KERNELS, NATIVE
+
+_CONFIG_DIR = Path(__file__).with_name("configs")
+_PROFILES = ("35b_tp1", "122b_tp4")
+_POLICIES = ("log_nearest", "nearby_equal_tiles")
+_NATIVE_TILE_W = (64, 128, 256)
+_NATIVE_TILE_T = (16, 32, 64, 128, 256)
+_SPLIT_MODES = ("none", "tail", "full")
+
+
+def available_profiles():
+    return _PROFILES
+
+
+def token_tile(entry):
+    """Token (M) tile of an entry, whatever the impl's key spelling (config.py:19-21)."""
+    c = entry["config"]
+    for key in ("BLOCK_T", "BLOCK_SIZE_M", "BM", "BT"):
+        if key in c:
+            return c[key]
+    return None
+
+
+def weight_tile(entry):
+    c = entry["config"]
+    for key in ("BLOCK_W", "BLOCK_SIZE_N", "BN"):
+        if key in c:
+            return c[key]
+    return None
+
+
+def _check_entry(field, nk, k, m, entry, policy):
+    where = f"{nk}/{m}"
+    if not 1 <= int(m) <= 16384 or entry.get("impl") not in KERNELS:
+        raise ValueError(f"Invalid entry: {where}")
+    c = entry["config"]
+    bt, bw = token_tile(entry), weight_tile(entry)
+    if entry["impl"] in NATIVE and "BLOCK_W" in c:
+        if bt not in _NATIVE_TILE_T or bw not in _NATIVE_TILE_W:
+            raise ValueError(f"Invalid tile: {where}")
+        if c.get("SPLIT_MODE", "full") not in _SPLIT_MODES:
+            raise ValueError(f"Invalid split mode: {where}")
+        waves = (c.get("WAVES_W"), c.get("WAVES_T"))
+        if waves != (None, None) and (None in waves or waves[0] * waves[1] != 4):
+            raise ValueError(f"Invalid wave grid: {where}")
+    elif not bt or bt & (bt - 1) or not bw or 128 % bw:
+        raise ValueError(f"Invalid tile: {where}")
+    if c.get("SPLIT", c.get("SPLIT_K", 1)) < 1:
+        raise ValueError(f"Invalid split-K: {where}")
+    if entry["impl"] == "shortk" and k != 256:
+        raise ValueError("shortk requires K=256")
+    if c.get("MODE") == 3 and (c["NUM_STAGES"] < 4 or (k // 128) % (4 * c.get("SPLIT", 1))):
+        raise ValueError("MODE=3 needs complete groups of four K tiles")
+    if field == "entries" and policy["kind"] == "nearby_equal_tiles":
+        us = entry.get("anchor_us")
+        if not isinstance(us, (int, float)) or not math.isfinite(us) or us <= 0:
+            raise ValueError("Measured anchor latency must be positive")
+
+
+def validate_config(data):
+    """Raise ValueError unless `data` is a well-formed schema-v1 profile (config.py:23-59)."""
+    if data.get("schema_version") != 1 or data.get("block_size") != [128, 128]:
+        raise ValueError("Unsupported schema or quantization block size")
+    if data.get("m_range") != [1, 16384]:
+        raise ValueError("Profiles must declare the validated M=1..16384 range")
+    shapes = {f"{s['N']},{s['K']}" for s in data["shapes"]}
+    if set(data["entries"]) != shapes:
+        raise ValueError("Shape inventory and dispatch entries disagree")
+    policy = data["policy"]
+    if policy.get("kind") not in _POLICIES:
+        raise ValueError("Unsupported dispatch policy")
+    if policy["kind"] == "nearby_equal_tiles":
+        if policy["max_distance"] < 0 or set(data.get("fallback_entries", {})) != shapes:
+            raise ValueError("Incomplete bounded interpolation/fallback policy")
+    for field in ("entries", "fallback_entries"):
+        for nk, table in data.get(field, {}).items():
+            n, k = (int(x) for x in nk.split(","))
+            if n % 128 or k % 128 or not table:
+                raise ValueError(f"Invalid shape/table: {nk}")
+            for m, entry in table.items():
+                _check_entry(field, nk, k, m, entry, policy)
+
+
+def load_profile(path):
+    """Read and validate a profile JSON from any path."""
+    data = json.loads(Path(path).read_text())
+    validate_config(data)
+    return data
+
+
+@lru_cache(maxsize=None)
+def _profile(name):
+    if name not in _PROFILES:
+        raise ValueError(f"Unknown profile {name!r}; choose one of {_PROFILES}")
+    return load_profile(_CONFIG_DIR / f"{name}.json")
+
+
+def get_profile(name):
+    return copy.deepcopy(_profile(name))
+
+
+def supports_in(data, m, n, k):
+    lo, hi = data["m_range"]
+    return lo <= m <= hi and f"{n},{k}" in data["entries"]
+
+
+def supports(profile, m, n, k):
+    return supports_in(_profile(profile), m, n, k)
+
+
+def _log_nearest(table, m):
+    # First minimum in JSON insertion order wins ties (config.py:100).
+    return min(table, key=lambda a: abs(math.log(int(a) / m)))
+
+
+def select_in(data, m, n, k):
+    """Policy of config.py:76-101 applied to a validated table dict.
+
+    Returns (entry, {"method": ..., "anchor": int}) without copying.
+    """
+    if not supports_in(data, m, n, k):
+        raise ValueError(f"{data.get('profile', 'profile')} does not cover M,N,K={m},{n},{k}")
+    nk = f"{n},{k}"
+    table = data["entries"][nk]
+    if str(m) in table:
+        return table[str(m)], {"method": "exact", "anchor": m}
+    policy = data["policy"]
+    if policy["kind"] == "nearby_equal_tiles":
+        best = None
+        for a, entry in table.items():
+            if entry["impl"] in policy["exact_only"]:
+                continue
+            anchor, bt = int(a), token_tile(entry)
+            if abs(m - anchor) > policy["max_distance"]:
+                continue
+            if -(-m // bt) != -(-anchor // bt):
+                continue
+            rank = (entry["anchor_us"], abs(math.log(m / anchor)), anchor)
+            if best is None or rank < best[0]:
+                best = (rank, anchor, entry)
+        if best is not None:
+            return best[2], {"method": "equal_tile_count", "anchor": best[1]}
+        table = data["fallback_entries"][nk]
+        method = "baseline_fallback"
+    else:
+        method = "log_nearest"
+    anchor = _log_nearest(table, m)
+    return table[anchor], {"method": method, "anchor": int(anchor)}
+
+
+@lru_cache(maxsize=4096)
+def _select(profile, m, n, k):
+    return select_in(_profile(profile), m, n, k)
+
+
+def select(profile, m, n, k):
+    """Return a copy of the selected entry and its routing explanation."""
+    return copy.deepcopy(_select(profile, m, n, k))

@@ -1,0 +1,496 @@
+// Block-scaled FP8 GEMM for AMD Instinct MI355X (gfx950): kernels + C ABI.
+//
+//   C[M,N] (bf16) = sum_g (A[:, g] . B[:, g]^T) * As[m, g] * Bs[n / 128, g]
+//
+// Math contract: reference fp8_gemm_h20/kernels/baseline_triton.py:16-18 and
+// scripts/validate.py:32-34 (fp32 accumulation, one 128-K scale group per
+// step, bf16 output).
+//
+// Design (gfx950, wave64):
+//  * MFMA v_mfma_f32_16x16x128_f8f6f4 (OCP e4m3 x e4m3 -> fp32).  One
+//    instruction covers a whole 128-K scale group of a 16x16 output block, so
+//    each group's product lands in a fresh fp32 register quad that is
+//    promoted immediately: acc = fma(p, As[m,g] * Bs[nb,g], acc).
+//  * Weights sit on the MFMA row side and tokens on the column side (the
+//    reference's SWAP_AB orientation, used here for every M).  A lane's four
+//    output values then share one token and one 128-row weight block, so the
+//    promotion factor is ONE fp32 scalar per lane per 16x16 block and group.
+//  * Workgroup = 256 threads = 4 waves.  A tile of block_w weight rows x
+//    block_t tokens x 128 K (one group) is staged global -> LDS with 16-byte
+//    loads, double-buffered across groups.  LDS rows are 128 bytes; 16-byte
+//    chunk c of row r is stored at chunk position c ^ (r & 7) so that the
+//    MFMA operand reads (8 consecutive lanes = 8 consecutive rows, same
+//    chunk) hit distinct banks.
+//  * Split-K: a tile's K range can be split over `split` workgroups that
+//    write fp32 partials to a caller-owned workspace; the last workgroup to
+//    arrive (agent-scope atomic counter) sums them in fixed split order and
+//    resets the counter, so results are bitwise reproducible and replayable
+//    in hipGraphs (same scheme as reference kernels/baseline_gluon.py:194-209).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fp8bg.h"
+
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr int kGroupK = 128;          // K elements per scale group
+constexpr int kRowBytes = kGroupK;    // one fp8 row of a group = 128 bytes
+constexpr int kMaxLds = 160 * 1024;   // gfx950 LDS per workgroup
+constexpr int kNumXcd = 8;            // MI355X: 8 XCDs, workgroups dealt round-robin
+
+struct KArgs {
+    const uint8_t* A;      // [M, K] e4m3, row stride K
+    const uint8_t* B;      // [N, K] e4m3, row stride K
+    const float* As;       // [M, K/128]
+    const float* Bs;       // [N/128, K/128]
+    uint16_t* C;           // [M, N] bf16, row stride N
+    float* ws;             // split-K partials
+    int* cnt;              // split-K arrival counters
+    int64_t as_sm, as_sk, bs_sn, bs_sk;
+    int M, N, K;
+    int tiles_w, tiles_t;
+    int n_dp;              // tiles computed whole
+    int split;             // workgroups per split tile
+    int group_t;           // token-tile swizzle group
+    int xcd_remap;
+    int scale_lds;
+};
+
+// fp32 -> bf16 bits, round to nearest even; any NaN -> 0x7fc0 (as torch).
+__device__ __forceinline__ uint32_t bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x128(const i32x8& w, const i32x8& t) {
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    // cbsz/blgp format 0 = OCP e4m3 for both operands; scale operands 0 =
+    // unscaled instruction.
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, t, zero, 0, 0, 0, 0, 0, 0);
+}
+
+// Bijective remap of workgroup ids 0..n-1 so that ids dealt to the same XCD
+// (id % 8) receive a contiguous run of logical tiles.
+__device__ __forceinline__ int xcd_remap(int pid, int n) {
+    const int per = n / kNumXcd, rem = n % kNumXcd;
+    const int xcd = pid % kNumXcd, local = pid / kNumXcd;
+    return xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
+template <int TW, int TT, int WW, int WT, int KF>
+__global__ __launch_bounds__(kThreads) void fp8bg_xdl(KArgs a) {
+    static_assert(WW * WT == kThreads / 64, "4 waves per workgroup");
+    constexpr int WTW = TW / WW;               // weight rows per wave
+    constexpr int WTT = TT / WT;               // tokens per wave
+    constexpr int NW = WTW / 16;               // 16-row weight blocks per wave
+    constexpr int NT = WTT / 16;               // 16-token blocks per wave
+    static_assert(WTW % 16 == 0 && WTT % 16 == 0 && NW >= 1 && NT >= 1, "wave tile");
+    static_assert(TW % 8 == 0 && TT % 8 == 0, "tile rows");
+    constexpr int ROWS = TW + TT;              // LDS rows per group buffer
+    constexpr int CHUNKS = ROWS * 8;           // 16-byte chunks per group
+    constexpr int NLD = (CHUNKS + kThreads - 1) / kThreads;
+    constexpr int WCH = TW * 8;                // chunks belonging to weights
+    constexpr int BUF = ROWS * kRowBytes;
+
+    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * BUF];
+    extern __shared__ float s_as[];            // [TT][kcount] when scale_lds
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wv_w = wave % WW, wv_t = wave / WW;
+
+    // ---- tile decode (reference baseline_gluon.py:109-126) ----
+    const int KG = KF ? KF : (a.K / kGroupK);
+    int pid = blockIdx.x;
+    int tile, sidx = 0, kcount, k_lo;
+    if (pid < a.n_dp) {
+        if (a.xcd_remap) pid = xcd_remap(pid, a.n_dp);
+        tile = pid;
+        k_lo = 0;
+        kcount = KG;
+    } else {
+        const int q = pid - a.n_dp;
+        tile = a.n_dp + q / a.split;
+        sidx = q % a.split;
+        kcount = KG / a.split;
+        k_lo = sidx * kcount;
+    }
+    const int per_group = a.group_t * a.tiles_w;
+    const int first_t = (tile / per_group) * a.group_t;
+    const int gsize = min(a.tiles_t - first_t, a.group_t);
+    const int pt = first_t + (tile % gsize);
+    const int pw = (tile % per_group) / gsize;
+    const int w0 = pw * TW, t0 = pt * TT;
+
+    // ---- per-thread global->LDS chunk assignment (fixed across groups) ----
+    // chunk c: row c/8 of the stacked [weights; tokens] tile, 16-byte column c%8.
+    const uint8_t* gptr[NLD];
+    int loff[NLD];
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+        const int c = tid + kThreads * j;
+        const int row = min(c >> 3, ROWS - 1);
+        const int col = c & 7;
+        if (kThreads * j < WCH) {
+            const int n = min(w0 + row, a.N - 1);
+            gptr[j] = a.B + (size_t)n * a.K + col * 16;
+        } else {
+            const int m = min(t0 + row - TW, a.M - 1);
+            gptr[j] = a.A + (size_t)m * a.K + col * 16;
+        }
+        loff[j] = row * kRowBytes + ((col ^ (row & 7)) << 4);
+    }
+    auto gload = [&](int g, i32x4 (&r)[NLD]) {
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            if (CHUNKS % kThreads == 0 || tid + kThreads * j < CHUNKS)
+                r[j] = *(const i32x4*)(gptr[j] + (size_t)g * kGroupK);
+        }
+    };
+    auto sstore = [&](int buf, const i32x4 (&r)[NLD]) {
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            if (CHUNKS % kThreads == 0 || tid + kThreads * j < CHUNKS)
+                *(i32x4*)(lds + buf * BUF + loff[j]) = r[j];
+        }
+    };
+
+    // ---- scales ----
+    // token of this lane in token block t; weight 128-block of weight block w
+    int tok[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) tok[t] = min(t0 + wv_t * WTT + t * 16 + (lane & 15), a.M - 1);
+    int nb[NW];
+    const int nblocks = a.N / 128;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) nb[w] = min((w0 + wv_w * WTW + w * 16) >> 7, nblocks - 1);
+
+    if (a.scale_lds) {
+        // Stage As[tile tokens, k_lo .. k_lo+kcount) once; walk memory along
+        // whichever As stride is unit so the loads coalesce.
+        const int n_el = TT * kcount;
+        if (a.as_sk == 1) {
+            for (int e = tid; e < n_el; e += kThreads) {
+                const int r = e / kcount, g = e % kcount;
+                const int m = min(t0 + r, a.M - 1);
+                s_as[r * kcount + g] = a.As[(int64_t)m * a.as_sm + (int64_t)(k_lo + g) * a.as_sk];
+            }
+        } else {
+            for (int e = tid; e < n_el; e += kThreads) {
+                const int g = e / TT, r = e % TT;
+                const int m = min(t0 + r, a.M - 1);
+                s_as[r * kcount + g] = a.As[(int64_t)m * a.as_sm + (int64_t)(k_lo + g) * a.as_sk];
+            }
+        }
+    }
+
+    float sa_n[NT], sb_n[NW];
+    auto sload = [&](int g, int i) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (a.scale_lds)
+                sa_n[t] = s_as[(tok[t] - t0) * kcount + i];
+            else
+                sa_n[t] = a.As[(int64_t)tok[t] * a.as_sm + (int64_t)g * a.as_sk];
+        }
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sb_n[w] = a.Bs[(int64_t)nb[w] * a.bs_sn + (int64_t)g * a.bs_sk];
+    };
+
+    f32x4 acc[NW][NT];
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[w][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    // Operand fetch: lane reads row (lane & 15) of a 16-row block, K bytes
+    // [32*(lane>>4), +32) of the group, as two swizzled 16-byte chunks.  The
+    // same K order is used for both operands, so the MFMA reduction is exact
+    // regardless of how the hardware orders K inside a lane.
+    const int c0 = ((lane >> 4) * 2) ^ (lane & 7);
+    auto opread = [&](int buf, int row) -> i32x8 {
+        const unsigned char* base = lds + buf * BUF + row * kRowBytes;
+        const i32x4 lo = *(const i32x4*)(base + (c0 << 4));
+        const i32x4 hi = *(const i32x4*)(base + ((c0 ^ 1) << 4));
+        return (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+
+    i32x4 stage[NLD];
+    if (a.scale_lds) __syncthreads();
+    gload(k_lo, stage);
+    sload(k_lo, 0);
+    sstore(0, stage);
+    __syncthreads();
+
+#pragma unroll (KF ? KF : 1)
+    for (int i = 0; i < kcount; ++i) {
+        const int g = k_lo + i;
+        const int buf = i & 1;
+        float sa[NT], sb[NW];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) sa[t] = sa_n[t];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sb[w] = sb_n[w];
+        const bool more = i + 1 < kcount;
+        if (more) {
+            gload(g + 1, stage);
+            sload(g + 1, i + 1);
+        }
+        i32x8 top[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) top[t] = opread(buf, TW + wv_t * WTT + t * 16 + (lane & 15));
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const i32x8 wop = opread(buf, wv_w * WTW + w * 16 + (lane & 15));
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const f32x4 p = mfma16x16x128(wop, top[t]);
+                const float s = sa[t] * sb[w];
+                acc[w][t][0] = __builtin_fmaf(p[0], s, acc[w][t][0]);
+                acc[w][t][1] = __builtin_fmaf(p[1], s, acc[w][t][1]);
+                acc[w][t][2] = __builtin_fmaf(p[2], s, acc[w][t][2]);
+                acc[w][t][3] = __builtin_fmaf(p[3], s, acc[w][t][3]);
+            }
+        }
+        if (more) sstore(buf ^ 1, stage);
+        __syncthreads();
+    }
+
+    // ---- epilogue ----
+    // Output block (w, t): this lane holds token (lane & 15) and the four
+    // consecutive weight rows 4*(lane >> 4) .. +3 -> one 8-byte bf16 store.
+    auto store_c = [&](const f32x4 (&v)[NW][NT]) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int m = t0 + wv_t * WTT + t * 16 + (lane & 15);
+            if (m >= a.M) continue;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const int n = w0 + wv_w * WTW + w * 16 + (lane >> 4) * 4;
+                if (n >= a.N) continue;
+                uint2 o;
+                o.x = bf16_bits(v[w][t][0]) | (bf16_bits(v[w][t][1]) << 16);
+                o.y = bf16_bits(v[w][t][2]) | (bf16_bits(v[w][t][3]) << 16);
+                *(uint2*)(a.C + (size_t)m * a.N + n) = o;
+            }
+        }
+    };
+
+    if (blockIdx.x < a.n_dp) {
+        store_c(acc);
+        return;
+    }
+
+    // Split tile: publish the partial, count arrivals, last one reduces.
+    const int stile = tile - a.n_dp;
+    constexpr int TILE_EL = TW * TT;
+    const int wave_off = wave * (WTW * WTT);
+    float* slab0 = a.ws + (size_t)stile * a.split * TILE_EL + wave_off;
+    {
+        float* mine = slab0 + (size_t)sidx * TILE_EL;
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                *(f32x4*)(mine + ((w * NT + t) * 64 + lane) * 4) = acc[w][t];
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(a.cnt + stile, 1, __ATOMIC_ACQ_REL,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (old == a.split - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    f32x4 tot[NW][NT];
+    for (int s = 0; s < a.split; ++s) {
+        const float* src = slab0 + (size_t)s * TILE_EL;
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const f32x4 v = (s == sidx) ? acc[w][t]
+                                            : *(const f32x4*)(src + ((w * NT + t) * 64 + lane) * 4);
+                if (s == 0)
+                    tot[w][t] = v;
+                else {
+                    tot[w][t][0] += v[0];
+                    tot[w][t][1] += v[1];
+                    tot[w][t][2] += v[2];
+                    tot[w][t][3] += v[3];
+                }
+            }
+    }
+    store_c(tot);
+    if (tid == 0) __hip_atomic_store(a.cnt + stile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Compiled instances: (block_w, block_t, waves_w, waves_t, k_fixed)
+// ---------------------------------------------------------------------------
+#define FP8BG_INSTANCES(X)                                                     \
+    X(64, 16, 4, 1, 0) X(128, 16, 4, 1, 0) X(256, 16, 4, 1, 0)                 \
+    X(64, 32, 4, 1, 0) X(128, 32, 4, 1, 0) X(256, 32, 4, 1, 0)                 \
+    X(64, 64, 4, 1, 0) X(128, 64, 4, 1, 0) X(256, 64, 4, 1, 0)                 \
+    X(128, 64, 2, 2, 0) X(128, 128, 2, 2, 0) X(128, 128, 4, 1, 0)              \
+    X(256, 128, 4, 1, 0) X(256, 128, 2, 2, 0) X(128, 256, 2, 2, 0)             \
+    X(64, 16, 4, 1, 2) X(128, 16, 4, 1, 2) X(64, 32, 4, 1, 2)                  \
+    X(128, 32, 4, 1, 2) X(128, 64, 4, 1, 2) X(128, 128, 2, 2, 2)               \
+    X(256, 128, 4, 1, 2)
+
+struct Instance {
+    int tw, tt, ww, wt, kf;
+    void (*launch)(dim3 grid, size_t shm, hipStream_t s, const KArgs& a);
+};
+
+#define FP8BG_LAUNCHER(TW, TT, WW, WT, KF)                                                   \
+    static void launch_##TW##_##TT##_##WW##_##WT##_##KF(dim3 g, size_t shm, hipStream_t s,  \
+                                                        const KArgs& a) {                   \
+        hipLaunchKernelGGL((fp8bg_xdl<TW, TT, WW, WT, KF>), g, dim3(kThreads), shm, s, a);  \
+    }
+FP8BG_INSTANCES(FP8BG_LAUNCHER)
+#undef FP8BG_LAUNCHER
+
+#define FP8BG_ENTRY(TW, TT, WW, WT, KF) {TW, TT, WW, WT, KF, launch_##TW##_##TT##_##WW##_##WT##_##KF},
+const Instance kInstances[] = {FP8BG_INSTANCES(FP8BG_ENTRY)};
+#undef FP8BG_ENTRY
+constexpr int kNumInstances = sizeof(kInstances) / sizeof(kInstances[0]);
+
+int find_instance(const fp8bg_config* c) {
+    for (int i = 0; i < kNumInstances; ++i) {
+        const Instance& k = kInstances[i];
+        if (k.tw == c->block_w && k.tt == c->block_t && k.ww == c->waves_w &&
+            k.wt == c->waves_t && k.kf == c->k_fixed)
+            return i;
+    }
+    return -1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fp8bg_version(void) { return 1; }
+
+const char* fp8bg_strerror(int code) {
+    switch (code) {
+        case FP8BG_OK: return "ok";
+        case FP8BG_ERR_SHAPE: return "invalid shape: need M>=1 and N, K positive multiples of 128";
+        case FP8BG_ERR_CONFIG: return "invalid or uncompiled kernel configuration";
+        case FP8BG_ERR_WORKSPACE: return "split-K workspace or counters missing or too small";
+        case FP8BG_ERR_ALIGN: return "A, B and C must be 16-byte aligned";
+        case FP8BG_ERR_LAUNCH: return "HIP kernel launch failed";
+        case FP8BG_ERR_DEVICE: return "HIP device query failed";
+        case FP8BG_ERR_NULL: return "required pointer argument is NULL";
+        default: return "unknown fp8bg error";
+    }
+}
+
+int fp8bg_num_cus(int device, int32_t* num_cus) {
+    if (!num_cus) return FP8BG_ERR_NULL;
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || v < 1)
+        return FP8BG_ERR_DEVICE;
+    *num_cus = v;
+    return FP8BG_OK;
+}
+
+int fp8bg_config_supported(const fp8bg_config* cfg) {
+    return cfg != nullptr && find_instance(cfg) >= 0;
+}
+
+int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, int32_t num_cus,
+                    fp8bg_plan* plan) {
+    if (!cfg || !plan) return FP8BG_ERR_NULL;
+    if (M < 1 || N < 128 || K < 128 || N % 128 || K % 128) return FP8BG_ERR_SHAPE;
+    const int ki = find_instance(cfg);
+    if (ki < 0) return FP8BG_ERR_CONFIG;
+    if (cfg->split < 1 || cfg->group_t < 1 || num_cus < 1) return FP8BG_ERR_CONFIG;
+    if (cfg->split_mode < FP8BG_SPLIT_NONE || cfg->split_mode > FP8BG_SPLIT_FULL) return FP8BG_ERR_CONFIG;
+    if (cfg->flags & ~(FP8BG_FLAG_SCALE_LDS | FP8BG_FLAG_XCD_REMAP)) return FP8BG_ERR_CONFIG;
+    const int kg = K / 128;
+    const Instance& k = kInstances[ki];
+    if (k.kf && kg != k.kf) return FP8BG_ERR_CONFIG;
+
+    int split = (cfg->split_mode == FP8BG_SPLIT_NONE || k.kf) ? 1 : cfg->split;
+    if (kg % split) split = 1;  // reference baseline_gluon.py:274-276
+    const int64_t tiles_w = (N + k.tw - 1) / k.tw;
+    const int64_t tiles_t = ((int64_t)M + k.tt - 1) / k.tt;
+    const int64_t tiles = tiles_w * tiles_t;
+    int64_t n_split = 0;
+    if (split > 1) n_split = cfg->split_mode == FP8BG_SPLIT_TAIL ? tiles % num_cus : tiles;
+    if (n_split == 0) split = 1;
+    const int64_t n_dp = tiles - n_split;
+    const int64_t grid = n_dp + n_split * split;
+    if (grid > 0x7fffffff) return FP8BG_ERR_SHAPE;
+    int64_t lds = 2LL * (k.tw + k.tt) * 128;
+    if (cfg->flags & FP8BG_FLAG_SCALE_LDS) lds += (int64_t)k.tt * kg * 4;
+    if (lds > kMaxLds) return FP8BG_ERR_CONFIG;
+
+    plan->tiles_w = (int32_t)tiles_w;
+    plan->tiles_t = (int32_t)tiles_t;
+    plan->tiles = (int32_t)tiles;
+    plan->split = split;
+    plan->n_dp = (int32_t)n_dp;
+    plan->n_split = (int32_t)n_split;
+    plan->grid = (int32_t)grid;
+    plan->cnt_elems = (int32_t)n_split;
+    plan->ws_elems = n_split * split * (int64_t)k.tw * k.tt;
+    plan->lds_bytes = (int32_t)lds;
+    plan->kernel_id = ki;
+    return FP8BG_OK;
+}
+
+int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_m,
+               int64_t as_stride_k, const float* Bs, int64_t bs_stride_n, int64_t bs_stride_k,
+               void* C, int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg,
+               int32_t num_cus, float* ws, int64_t ws_elems, int32_t* cnt, int32_t cnt_elems,
+               void* stream) {
+    if (!A || !B || !As || !Bs || !C) return FP8BG_ERR_NULL;
+    fp8bg_plan p;
+    const int rc = fp8bg_make_plan(M, N, K, cfg, num_cus, &p);
+    if (rc != FP8BG_OK) return rc;
+    if ((((uintptr_t)A) | ((uintptr_t)B) | ((uintptr_t)C)) & 15) return FP8BG_ERR_ALIGN;
+    if (p.n_split > 0 && (!ws || !cnt || ws_elems < p.ws_elems || cnt_elems < p.cnt_elems))
+        return FP8BG_ERR_WORKSPACE;
+
+    KArgs a;
+    a.A = (const uint8_t*)A;
+    a.B = (const uint8_t*)B;
+    a.As = As;
+    a.Bs = Bs;
+    a.C = (uint16_t*)C;
+    a.ws = ws;
+    a.cnt = cnt;
+    a.as_sm = as_stride_m;
+    a.as_sk = as_stride_k;
+    a.bs_sn = bs_stride_n;
+    a.bs_sk = bs_stride_k;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.tiles_w = p.tiles_w;
+    a.tiles_t = p.tiles_t;
+    a.n_dp = p.n_dp;
+    a.split = p.split;
+    a.group_t = cfg->group_t;
+    a.xcd_remap = (cfg->flags & FP8BG_FLAG_XCD_REMAP) ? 1 : 0;
+    a.scale_lds = (cfg->flags & FP8BG_FLAG_SCALE_LDS) ? 1 : 0;
+    const Instance& k = kInstances[p.kernel_id];
+    const size_t shm = a.scale_lds ? (size_t)k.tt * (K / 128) * sizeof(float) : 0;
+    k.launch(dim3(p.grid), shm, (hipStream_t)stream, a);
+    return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
+}
+
+}  // extern "C"

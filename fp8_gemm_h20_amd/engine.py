@@ -1,0 +1,37 @@
+"""One kernel registry shared by all profiles (reference fp8_gemm_h20/engine.py:5-19).
+
+`KERNELS[impl] = (module, function)`; the function is imported on first use,
+so importing the package and selecting configs neither loads libfp8bg.so nor
+touches the GPU.  `run(entry, args)` calls fn(A, B, As, Bs, dict(config)).
+
+gfx950-native impls written by this package's tables:
+  xdl     LDS-tiled MFMA kernel, tail or full split-K
+  shortk  K == 256 kernel, no K loop (also accepts the reference's BM/BN keys)
+Reference H20 impl names, accepted so reference tables keep working; each
+runs on the gfx950 kernels (see kernels.py):
+  triton, gluon, v2, scale_tma
+"""
+from functools import lru_cache
+from importlib import import_module
+
+KERNELS = {
+    "xdl": ("kernels", "xdl"),
+    "shortk": ("kernels", "shortk"),
+    "triton": ("kernels", "triton"),
+    "gluon": ("kernels", "gluon"),
+    "v2": ("kernels", "v2"),
+    "scale_tma": ("kernels", "scale_tma"),
+}
+
+# impls whose config uses this package's gfx950 keys
+NATIVE = ("xdl", "shortk")
+
+
+@lru_cache(maxsize=None)
+def kernel(name):
+    module, function = KERNELS[name]
+    return getattr(import_module(f".{module}", __package__), function)
+
+
+def run(entry, args):
+    return kernel(entry["impl"])(*args, dict(entry["config"]))

@@ -1,0 +1,220 @@
+"""Host functions of the kernel registry: fn(A, B, As, Bs, config) -> C.
+
+Each function keeps the reference's L0 wrapper contract
+(fp8_gemm_h20/engine.py:18-19): A[M,K], B[N,K] contiguous e4m3fn CUDA tensors,
+As[M,K/128] and Bs[N/128,K/128] fp32 with any strides, `config` a plain dict;
+it allocates C = empty(M, N, bf16) on A's device, enqueues one HIP kernel on
+the current stream through the C ABI (include/fp8bg.h) and returns C without
+synchronising.
+
+Two families of config dicts are accepted:
+
+* gfx950-native entries (impl "xdl", "shortk") written by this package's
+  tuner: BLOCK_W, BLOCK_T, WAVES_W, WAVES_T, SPLIT, SPLIT_MODE,
+  GROUP_SIZE_M, SCALE_LDS, XCD_REMAP.
+* the reference's H20 entries (impl "triton", "gluon", "v2", "scale_tma",
+  "shortk" with BM/BN keys), translated onto the nearest compiled gfx950 tile
+  so that an existing reference profile table still runs unchanged.
+"""
+import ctypes
+from functools import lru_cache
+
+from . import _lib
+
+# (block_w, block_t, waves_w, waves_t, k_fixed) compiled into libfp8bg.so;
+# must equal FP8BG_INSTANCES in csrc/fp8bg.hip (checked by tests).
+INSTANCES = (
+    (64, 16, 4, 1, 0), (128, 16, 4, 1, 0), (256, 16, 4, 1, 0),
+    (64, 32, 4, 1, 0), (128, 32, 4, 1, 0), (256, 32, 4, 1, 0),
+    (64, 64, 4, 1, 0), (128, 64, 4, 1, 0), (256, 64, 4, 1, 0),
+    (128, 64, 2, 2, 0), (128, 128, 2, 2, 0), (128, 128, 4, 1, 0),
+    (256, 128, 4, 1, 0), (256, 128, 2, 2, 0), (128, 256, 2, 2, 0),
+    (64, 16, 4, 1, 2), (128, 16, 4, 1, 2), (64, 32, 4, 1, 2),
+    (128, 32, 4, 1, 2), (128, 64, 4, 1, 2), (128, 128, 2, 2, 2),
+    (256, 128, 4, 1, 2),
+)
+
+SPLIT_MODES = {"none": _lib.SPLIT_NONE, "tail": _lib.SPLIT_TAIL, "full": _lib.SPLIT_FULL}
+TILE_W = (64, 128, 256)
+TILE_T = (16, 32, 64, 128, 256)
+
+
+def default_waves(block_w, block_t, k_fixed=0):
+    """Wave grid of the first compiled instance with this tile."""
+    for tw, tt, ww, wt, kf in INSTANCES:
+        if (tw, tt, kf) == (block_w, block_t, k_fixed):
+            return ww, wt
+    return None
+
+
+def is_compiled(block_w, block_t, waves_w, waves_t, k_fixed=0):
+    return (block_w, block_t, waves_w, waves_t, k_fixed) in INSTANCES
+
+
+def nearest_tile(block_w, block_t, k_fixed=0):
+    """Closest compiled (block_w, block_t) for a requested tile.
+
+    Used to run reference (H20) table entries: their tiles (16..64 wide)
+    are sized for 78 SMs and warp-level wgmma; gfx950 tiles start at 64 weight
+    rows.  Preference: keep the token tile, then the nearest weight tile.
+    """
+    best = None
+    for tw, tt, _, _, kf in INSTANCES:
+        if kf != k_fixed:
+            continue
+        cost = (abs((tt or 1).bit_length() - max(block_t, 1).bit_length()) * 4
+                + abs(tw.bit_length() - max(block_w, 1).bit_length()))
+        if best is None or cost < best[0]:
+            best = (cost, tw, tt)
+    return best[1], best[2]
+
+
+def native_struct(cfg, k_fixed=0):
+    """Build the C config struct from a gfx950-native config dict."""
+    tw, tt = int(cfg["BLOCK_W"]), int(cfg["BLOCK_T"])
+    ww, wt = cfg.get("WAVES_W"), cfg.get("WAVES_T")
+    if ww is None or wt is None:
+        waves = default_waves(tw, tt, k_fixed)
+        if waves is None:
+            raise ValueError(f"no compiled gfx950 kernel for tile {tw}x{tt} (k_fixed={k_fixed})")
+        ww, wt = waves
+    mode = cfg.get("SPLIT_MODE", "full")
+    if mode not in SPLIT_MODES:
+        raise ValueError(f"SPLIT_MODE must be one of {tuple(SPLIT_MODES)}")
+    flags = 0
+    if cfg.get("SCALE_LDS", False):
+        flags |= _lib.FLAG_SCALE_LDS
+    if cfg.get("XCD_REMAP", False):
+        flags |= _lib.FLAG_XCD_REMAP
+    return _lib.Config(tw, tt, int(ww), int(wt), int(cfg.get("SPLIT", 1)), SPLIT_MODES[mode],
+                       int(cfg.get("GROUP_SIZE_M", 1)), flags, k_fixed)
+
+
+# ---------------------------------------------------------------------------
+# device state: CU count and split-K buffers
+# ---------------------------------------------------------------------------
+_NUM_CUS = {}
+# Split-K workspace + counters keyed by (device, stream): launches on one
+# stream are ordered, so reuse is safe; kernels on different streams never
+# share buffers (reference baseline_gluon.py:229-244).  Counters start at
+# zero and every kernel leaves them zero, so hipGraph replay is safe.
+_BUFS = {}
+
+
+def _device_index(dev):
+    import torch
+    return dev.index if dev.index is not None else torch.cuda.current_device()
+
+
+def num_cus(dev):
+    idx = _device_index(dev)
+    n = _NUM_CUS.get(idx)
+    if n is None:
+        n = _NUM_CUS[idx] = _lib.num_cus(idx)
+    return n
+
+
+def _bufs(dev, ws_elems, cnt_elems):
+    import torch
+    key = (_device_index(dev), torch.cuda.current_stream(dev).cuda_stream)
+    ws, cnt = _BUFS.get(key, (None, None))
+    if ws is None or ws.numel() < ws_elems:
+        ws = torch.empty(max(ws_elems, 1 << 20), device=dev, dtype=torch.float32)
+    if cnt is None or cnt.numel() < cnt_elems:
+        cnt = torch.zeros(max(cnt_elems, 4096), device=dev, dtype=torch.int32)
+    _BUFS[key] = (ws, cnt)
+    return ws, cnt
+
+
+def launch(A, B, As, Bs, cstruct):
+    """Allocate C and enqueue the kernel described by `cstruct`."""
+    import torch
+    M, K = A.shape
+    N = B.shape[0]
+    dev = A.device
+    cus = num_cus(dev)
+    plan = _lib.make_plan(M, N, K, cstruct, cus)
+    C = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+    ws_ptr = cnt_ptr = None
+    ws_n = cnt_n = 0
+    if plan.n_split:
+        ws, cnt = _bufs(dev, plan.ws_elems, plan.cnt_elems)
+        ws_ptr, cnt_ptr, ws_n, cnt_n = ws.data_ptr(), cnt.data_ptr(), ws.numel(), cnt.numel()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    _lib.check(_lib.lib().fp8bg_gemm(
+        A.data_ptr(), B.data_ptr(),
+        As.data_ptr(), As.stride(0), As.stride(1),
+        Bs.data_ptr(), Bs.stride(0), Bs.stride(1),
+        C.data_ptr(), M, N, K, ctypes.byref(cstruct), cus,
+        ws_ptr, ws_n, cnt_ptr, cnt_n, stream))
+    return C
+
+
+@lru_cache(maxsize=1024)
+def _native_cached(items, k_fixed):
+    return native_struct(dict(items), k_fixed)
+
+
+def _freeze(config):
+    return tuple(sorted(config.items()))
+
+
+# ---------------------------------------------------------------------------
+# gfx950-native impls
+# ---------------------------------------------------------------------------
+def xdl(A, B, As, Bs, config):
+    """LDS-tiled MFMA kernel with optional tail/full split-K."""
+    return launch(A, B, As, Bs, _native_cached(_freeze(config), 0))
+
+
+def shortk(A, B, As, Bs, config):
+    """K == 256 kernel: both scale groups unrolled, no K loop, no split-K.
+
+    Accepts gfx950 keys (BLOCK_W/BLOCK_T) or the reference's shortk keys
+    (BM/BN, kernels/kernel_shortk.py:46-54)."""
+    K = A.shape[1]
+    if K != 256:
+        raise ValueError("shortk requires K=256")
+    if "BLOCK_W" not in config:
+        tw, tt = nearest_tile(int(config["BN"]), int(config["BM"]), k_fixed=2)
+        config = {"BLOCK_W": tw, "BLOCK_T": tt, "GROUP_SIZE_M": int(config.get("GROUP", 1))}
+    return launch(A, B, As, Bs, _native_cached(_freeze(config), 2))
+
+
+# ---------------------------------------------------------------------------
+# reference (H20) table entries on gfx950 kernels
+# ---------------------------------------------------------------------------
+def _compat(tw_req, tt_req, split, mode, group, scale_lds=False):
+    tw, tt = nearest_tile(tw_req, tt_req)
+    cfg = {"BLOCK_W": tw, "BLOCK_T": tt, "SPLIT": int(split), "SPLIT_MODE": mode,
+           "GROUP_SIZE_M": int(group), "SCALE_LDS": bool(scale_lds)}
+    return _native_cached(_freeze(cfg), 0)
+
+
+def triton(A, B, As, Bs, config):
+    """Reference c3 entry (kernels/baseline_triton.py:87-114): full-grid split-K."""
+    c = _compat(config["BLOCK_SIZE_N"], config["BLOCK_SIZE_M"], config.get("SPLIT_K", 1), "full",
+                config.get("GROUP_SIZE_M", 1))
+    return launch(A, B, As, Bs, c)
+
+
+def gluon(A, B, As, Bs, config):
+    """Reference c11 entry (kernels/baseline_gluon.py:259-293): tail split-K."""
+    c = _compat(config["BLOCK_W"], config["BLOCK_T"], config.get("SPLIT", 1), "tail",
+                config.get("GROUP_SIZE_M", 1))
+    return launch(A, B, As, Bs, c)
+
+
+def v2(A, B, As, Bs, config):
+    """Reference v2 entry (kernels/kernel_v2.py:339-376): same schedule as c11."""
+    return gluon(A, B, As, Bs, config)
+
+
+def scale_tma(A, B, As, Bs, config):
+    """Reference scale-TMA entry (kernels/kernel_scale_tma.py:356-396).
+
+    Stages As in LDS when As is row-major, and otherwise runs the v2 path,
+    mirroring the reference's `As.stride(1) != 1` fallback (:367-369)."""
+    c = _compat(config["BLOCK_W"], config["BLOCK_T"], config.get("SPLIT", 1), "tail",
+                config.get("GROUP_SIZE_M", 1), scale_lds=As.stride(1) == 1)
+    return launch(A, B, As, Bs, c)

@@ -1,0 +1,143 @@
+/*
+ * fp8bg.h - C ABI of the gfx950 block-scaled FP8 GEMM library (libfp8bg.so).
+ *
+ * Computes, on one AMD Instinct MI355X (gfx950):
+ *
+ *     C[M,N] (bf16) = sum_g ( A[:, g] . B[:, g]^T ) * As[m, g] * Bs[n / 128, g]
+ *
+ * where g runs over the K/128 groups of 128 K elements, A[M,K] and B[N,K] are
+ * OCP e4m3 ("float8_e4m3fn") row-major with row stride K, As[M,K/128] and
+ * Bs[N/128,K/128] are fp32 with arbitrary element strides, and C is row-major
+ * bf16 with row stride N (round-to-nearest-even from the fp32 accumulator).
+ *
+ * The reference (qiuuuuu622/fp8_gemm_h20) has no C ABI: its kernels are
+ * Python-level Triton/Gluon host wrappers with the signature
+ *     fn(A, B, As, Bs, config: dict) -> C
+ * registered in fp8_gemm_h20/engine.py:5-19.  Each entry point below names the
+ * reference interface it replaces.  All pointers are device pointers except
+ * the config/plan structs and output scalars; no torch types cross this ABI.
+ * Every function is reentrant; the library owns no device allocations.
+ */
+#ifndef FP8BG_H
+#define FP8BG_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes (returned by every entry point; 0 = success) ---------- */
+#define FP8BG_OK             0
+#define FP8BG_ERR_SHAPE      1  /* M<1, N or K not a positive multiple of 128, ... */
+#define FP8BG_ERR_CONFIG     2  /* tile/wave/split combination not built or invalid */
+#define FP8BG_ERR_WORKSPACE  3  /* split-K workspace or counters missing/too small */
+#define FP8BG_ERR_ALIGN      4  /* A, B or C not 16-byte aligned */
+#define FP8BG_ERR_LAUNCH     5  /* hipLaunchKernel / hip runtime error */
+#define FP8BG_ERR_DEVICE     6  /* device query failed */
+#define FP8BG_ERR_NULL       7  /* required pointer argument is NULL */
+
+/* ---- split-K modes ------------------------------------------------------ */
+/* No split: every tile runs the full K range (config SPLIT ignored). */
+#define FP8BG_SPLIT_NONE 0
+/* Tail split (reference kernels/baseline_gluon.py:274-287): the first
+ * tiles - (tiles % num_cus) tiles run whole; only the last partial wave is
+ * split over `split` workgroups whose fp32 partials are summed in fixed
+ * split order by the last-arriving workgroup. */
+#define FP8BG_SPLIT_TAIL 1
+/* Full split (reference kernels/baseline_triton.py:100-114): every tile is
+ * split; same deterministic fixed-order in-kernel reduction. */
+#define FP8BG_SPLIT_FULL 2
+
+/* ---- config flags --------------------------------------------------------- */
+/* Stage the tile's activation scales As[tile rows, k range] in LDS once per
+ * workgroup (reference kernels/kernel_scale_tma.py:160-165); any As strides. */
+#define FP8BG_FLAG_SCALE_LDS 0x1
+/* Remap workgroup ids so that consecutive tiles run on the same XCD (L2). */
+#define FP8BG_FLAG_XCD_REMAP 0x2
+
+/*
+ * Kernel configuration: one gfx950 table entry (fp8_gemm_h20_amd/configs/*.json).
+ * Replaces the reference's per-entry `config` dict (fp8_gemm_h20/config.py:80-91).
+ */
+typedef struct fp8bg_config {
+    int32_t block_w;    /* weight rows (N) per workgroup tile: 64, 128 or 256 */
+    int32_t block_t;    /* tokens (M) per workgroup tile: 16 .. 256, power of 2 */
+    int32_t waves_w;    /* waves along N inside the tile (waves_w*waves_t == 4) */
+    int32_t waves_t;    /* waves along M inside the tile */
+    int32_t split;      /* K split factor, in 128-K groups; normalised to 1 when
+                           it does not divide K/128 (baseline_gluon.py:274-276) */
+    int32_t split_mode; /* FP8BG_SPLIT_* */
+    int32_t group_t;    /* token-tile swizzle group (GROUP_SIZE_M semantics,
+                           baseline_triton.py:36-45); >= 1 */
+    int32_t flags;      /* FP8BG_FLAG_* */
+    int32_t k_fixed;    /* 0 = runtime K loop; 2 = K==256 short-K kernel with no
+                           K loop (reference kernels/kernel_shortk.py:11-54) */
+} fp8bg_config;
+
+/*
+ * Launch plan derived on the host from (M,N,K,config,num_cus).  Pure host
+ * arithmetic: CPU-testable without a GPU.
+ * Replaces the host-wrapper arithmetic of kernels/baseline_gluon.py:266-287
+ * (split normalisation, tail = tiles % num_SMs, n_dp, grid, _bufs sizes).
+ */
+typedef struct fp8bg_plan {
+    int32_t tiles_w;    /* ceil(N / block_w) */
+    int32_t tiles_t;    /* ceil(M / block_t) */
+    int32_t tiles;      /* tiles_w * tiles_t */
+    int32_t split;      /* effective split (1 when not split) */
+    int32_t n_dp;       /* tiles computed whole (no reduction) */
+    int32_t n_split;    /* tiles split over `split` workgroups */
+    int32_t grid;       /* workgroups launched = n_dp + n_split * split */
+    int32_t cnt_elems;  /* int32 arrival counters needed (0 if no split) */
+    int64_t ws_elems;   /* fp32 workspace elements needed (0 if no split) */
+    int32_t lds_bytes;  /* LDS used per workgroup */
+    int32_t kernel_id;  /* index of the compiled kernel instance */
+} fp8bg_plan;
+
+/* Library ABI version (bumped on any signature or struct change). */
+int fp8bg_version(void);
+
+/* Number of compute units of `device` (replaces _num_sms,
+ * kernels/baseline_gluon.py:218-226). */
+int fp8bg_num_cus(int device, int32_t* num_cus);
+
+/* Validate (M,N,K,config) and fill `plan`.  No device calls. */
+int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg,
+                    int32_t num_cus, fp8bg_plan* plan);
+
+/* 1 if this tile/wave/k_fixed combination is compiled into the library. */
+int fp8bg_config_supported(const fp8bg_config* cfg);
+
+/*
+ * The GEMM.  Enqueues one kernel on `stream` (a hipStream_t; NULL = default
+ * stream) and returns without synchronising.  Replaces the L0 host wrappers
+ *   block_fp8_gemm_triton_h20  (kernels/baseline_triton.py:87-114)
+ *   block_fp8_gemm_gluon_h20   (kernels/baseline_gluon.py:259-293)
+ *   block_fp8_gemm_v2          (kernels/kernel_v2.py:339-376)
+ *   block_fp8_gemm_scale_tma   (kernels/kernel_scale_tma.py:356-396)
+ *   shortk                     (kernels/kernel_shortk.py:46-54)
+ * with the caller owning C (bf16 [M,N], row stride N), the fp32 split-K
+ * workspace `ws` (>= plan.ws_elems) and the int32 counters `cnt`
+ * (>= plan.cnt_elems, zero before the first call; every call leaves them
+ * zero again, so calls may be captured in a hipGraph and replayed).
+ * Calls that share `ws`/`cnt` must be ordered (same stream).
+ * Scale strides are in elements.  A, B and C must be 16-byte aligned.
+ */
+int fp8bg_gemm(const void* A, const void* B,
+               const float* As, int64_t as_stride_m, int64_t as_stride_k,
+               const float* Bs, int64_t bs_stride_n, int64_t bs_stride_k,
+               void* C, int32_t M, int32_t N, int32_t K,
+               const fp8bg_config* cfg, int32_t num_cus,
+               float* ws, int64_t ws_elems, int32_t* cnt, int32_t cnt_elems,
+               void* stream);
+
+/* Static message for an error code. */
+const char* fp8bg_strerror(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FP8BG_H */
