@@ -94,10 +94,50 @@ def native_struct(cfg, k_fixed=0):
 # device state: CU count and split-K buffers
 # ---------------------------------------------------------------------------
 _NUM_CUS = {}
-# Split-K workspace + counters keyed by (device, stream): launches on one
-# stream are ordered, so reuse is safe; kernels on different streams never
-# share buffers (reference baseline_gluon.py:229-244).  Counters start at
-# zero and every kernel leaves them zero, so hipGraph replay is safe.
+
+
+class SplitBuffers:
+    """Split-K workspace (fp32) and arrival counters (int32) of one
+    (device, stream) pair (reference baseline_gluon.py:229-244).
+
+    Launches on one stream are ordered, so every split-K GEMM on that stream
+    can share one workspace; kernels on different streams never share.
+    Counters start at zero and every kernel leaves them zero, so captured
+    hipGraphs can be replayed.
+
+    Growth never frees a buffer: a hipGraph captured earlier holds the old
+    device addresses, and torch.cuda.graph() empties the allocator cache at
+    every capture, which would hand freed blocks back to the driver and leave
+    such a graph writing to unmapped memory.  Replaced buffers are therefore
+    retired (kept alive until the process ends); sizes at least double on each
+    growth, so the retired total stays below the live size.
+    """
+
+    MIN_WS = 1 << 20
+    MIN_CNT = 4096
+
+    def __init__(self, device):
+        self.device = device
+        self.ws = None
+        self.cnt = None
+        self.retired = []
+
+    def get(self, ws_elems, cnt_elems):
+        import torch
+        if self.ws is None or self.ws.numel() < ws_elems:
+            size = max(ws_elems, self.MIN_WS, 2 * (self.ws.numel() if self.ws is not None else 0))
+            if self.ws is not None:
+                self.retired.append(self.ws)
+            self.ws = torch.empty(size, device=self.device, dtype=torch.float32)
+        if self.cnt is None or self.cnt.numel() < cnt_elems:
+            size = max(cnt_elems, self.MIN_CNT, 2 * (self.cnt.numel() if self.cnt is not None else 0))
+            if self.cnt is not None:
+                self.retired.append(self.cnt)
+            self.cnt = torch.zeros(size, device=self.device, dtype=torch.int32)
+        return self.ws, self.cnt
+
+
+# (device index, stream handle) -> SplitBuffers
 _BUFS = {}
 
 
@@ -117,13 +157,10 @@ def num_cus(dev):
 def _bufs(dev, ws_elems, cnt_elems):
     import torch
     key = (_device_index(dev), torch.cuda.current_stream(dev).cuda_stream)
-    ws, cnt = _BUFS.get(key, (None, None))
-    if ws is None or ws.numel() < ws_elems:
-        ws = torch.empty(max(ws_elems, 1 << 20), device=dev, dtype=torch.float32)
-    if cnt is None or cnt.numel() < cnt_elems:
-        cnt = torch.zeros(max(cnt_elems, 4096), device=dev, dtype=torch.int32)
-    _BUFS[key] = (ws, cnt)
-    return ws, cnt
+    bufs = _BUFS.get(key)
+    if bufs is None:
+        bufs = _BUFS[key] = SplitBuffers(dev)
+    return bufs.get(ws_elems, cnt_elems)
 
 
 def launch(A, B, As, Bs, cstruct):
