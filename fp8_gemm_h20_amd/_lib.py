@@ -11,7 +11,7 @@ from pathlib import Path
 
 LIB_NAME = "libfp8bg.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK = 0
 ERR_SHAPE = 1
@@ -21,6 +21,9 @@ ERR_ALIGN = 4
 ERR_LAUNCH = 5
 ERR_DEVICE = 6
 ERR_NULL = 7
+
+KIND_TILED = 0
+KIND_SKINNY = 1
 
 SPLIT_NONE = 0
 SPLIT_TAIL = 1
@@ -43,10 +46,13 @@ EXPORTS = (
 class Config(ctypes.Structure):
     """struct fp8bg_config."""
     _fields_ = [
+        ("kind", ctypes.c_int32),
         ("block_w", ctypes.c_int32),
         ("block_t", ctypes.c_int32),
         ("waves_w", ctypes.c_int32),
         ("waves_t", ctypes.c_int32),
+        ("waves_k", ctypes.c_int32),
+        ("unroll", ctypes.c_int32),
         ("split", ctypes.c_int32),
         ("split_mode", ctypes.c_int32),
         ("group_t", ctypes.c_int32),
@@ -65,9 +71,10 @@ class Plan(ctypes.Structure):
         ("n_dp", ctypes.c_int32),
         ("n_split", ctypes.c_int32),
         ("grid", ctypes.c_int32),
-        ("cnt_elems", ctypes.c_int32),
+        ("launches", ctypes.c_int32),
         ("ws_elems", ctypes.c_int64),
         ("lds_bytes", ctypes.c_int32),
+        ("threads", ctypes.c_int32),
         ("kernel_id", ctypes.c_int32),
     ]
 
@@ -100,7 +107,7 @@ def _declare(lib):
         vp, i64, i64,           # Bs, strides
         vp, i32, i32, i32,      # C, M, N, K
         ctypes.POINTER(Config), i32,
-        vp, i64, vp, i32,       # ws, ws_elems, cnt, cnt_elems
+        vp, i64,                # ws, ws_elems
         vp,                     # stream
     ]
     lib.fp8bg_gemm.restype = ctypes.c_int

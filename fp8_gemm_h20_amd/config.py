@@ -7,11 +7,12 @@ no GPU: only json/math/copy/functools.
 
 Differences, all additive:
 * Packaged tables (configs/*.json) are gfx950 tables whose entries use the
-  native impls "xdl"/"shortk".  Their tile rule is widened: BLOCK_W in
-  {64, 128, 256} (a 256-row tile spans two 128-row weight-scale blocks) and
-  BLOCK_T a power of two in 16..256.  Entries with the reference's impl
-  names keep the reference's rule (BLOCK_W divides 128, power-of-two token
-  tile), so the reference's own H20 tables validate and route unchanged.
+  native impls "tiled"/"skinny"/"shortk".  Their tile rule is widened: a
+  native entry must name a kernel instance compiled into libfp8bg.so (e.g. a
+  256-row tiled tile spans two 128-row weight-scale blocks).  Entries with
+  the reference's impl names keep the reference's rule (BLOCK_W divides 128,
+  power-of-two token tile), so the reference's own H20 tables validate and
+  route unchanged.
 * `select_in(data, M, N, K)` / `supports_in(...)` apply the policy to any
   validated table dict, e.g. a table loaded with `load_profile(path)`.
 """
@@ -26,8 +27,6 @@ from .engine import KERNELS, NATIVE
 _CONFIG_DIR = Path(__file__).with_name("configs")
 _PROFILES = ("35b_tp1", "122b_tp4")
 _POLICIES = ("log_nearest", "nearby_equal_tiles")
-_NATIVE_TILE_W = (64, 128, 256)
-_NATIVE_TILE_T = (16, 32, 64, 128, 256)
 _SPLIT_MODES = ("none", "tail", "full")
 
 
@@ -52,6 +51,23 @@ def weight_tile(entry):
     return None
 
 
+def _native_ok(impl, c, k):
+    """A gfx950-native entry names a compiled kernel instance."""
+    from .kernels import TILED, SKINNY_TILES
+    tw, tt = c.get("BLOCK_W"), c.get("BLOCK_T")
+    if impl == "skinny":
+        mode = c.get("SPLIT_MODE", "none")
+        return (mode in ("none", "full") and
+                (tw, tt, c.get("WAVES_K", 8), c.get("UNROLL", 1)) in SKINNY_TILES)
+    kf = 2 if impl == "shortk" else 0
+    if c.get("SPLIT_MODE", "full") not in _SPLIT_MODES:
+        return False
+    waves = (c.get("WAVES_W"), c.get("WAVES_T"))
+    if waves == (None, None):
+        return any((w, t, f) == (tw, tt, kf) for w, t, _, _, f in TILED)
+    return (tw, tt, waves[0], waves[1], kf) in TILED
+
+
 def _check_entry(field, nk, k, m, entry, policy):
     where = f"{nk}/{m}"
     if not 1 <= int(m) <= 16384 or entry.get("impl") not in KERNELS:
@@ -59,13 +75,8 @@ def _check_entry(field, nk, k, m, entry, policy):
     c = entry["config"]
     bt, bw = token_tile(entry), weight_tile(entry)
     if entry["impl"] in NATIVE and "BLOCK_W" in c:
-        if bt not in _NATIVE_TILE_T or bw not in _NATIVE_TILE_W:
+        if not _native_ok(entry["impl"], c, k):
             raise ValueError(f"Invalid tile: {where}")
-        if c.get("SPLIT_MODE", "full") not in _SPLIT_MODES:
-            raise ValueError(f"Invalid split mode: {where}")
-        waves = (c.get("WAVES_W"), c.get("WAVES_T"))
-        if waves != (None, None) and (None in waves or waves[0] * waves[1] != 4):
-            raise ValueError(f"Invalid wave grid: {where}")
     elif not bt or bt & (bt - 1) or not bw or 128 % bw:
         raise ValueError(f"Invalid tile: {where}")
     if c.get("SPLIT", c.get("SPLIT_K", 1)) < 1:

@@ -6,26 +6,36 @@
 // scripts/validate.py:32-34 (fp32 accumulation, one 128-K scale group per
 // step, bf16 output).
 //
-// Design (gfx950, wave64):
-//  * MFMA v_mfma_f32_16x16x128_f8f6f4 (OCP e4m3 x e4m3 -> fp32).  One
-//    instruction covers a whole 128-K scale group of a 16x16 output block, so
-//    each group's product lands in a fresh fp32 register quad that is
-//    promoted immediately: acc = fma(p, As[m,g] * Bs[nb,g], acc).
-//  * Weights sit on the MFMA row side and tokens on the column side (the
-//    reference's SWAP_AB orientation, used here for every M).  A lane's four
-//    output values then share one token and one 128-row weight block, so the
-//    promotion factor is ONE fp32 scalar per lane per 16x16 block and group.
-//  * Workgroup = 256 threads = 4 waves.  A tile of block_w weight rows x
-//    block_t tokens x 128 K (one group) is staged global -> LDS with 16-byte
-//    loads, double-buffered across groups.  LDS rows are 128 bytes; 16-byte
-//    chunk c of row r is stored at chunk position c ^ (r & 7) so that the
-//    MFMA operand reads (8 consecutive lanes = 8 consecutive rows, same
-//    chunk) hit distinct banks.
-//  * Split-K: a tile's K range can be split over `split` workgroups that
-//    write fp32 partials to a caller-owned workspace; the last workgroup to
-//    arrive (agent-scope atomic counter) sums them in fixed split order and
-//    resets the counter, so results are bitwise reproducible and replayable
-//    in hipGraphs (same scheme as reference kernels/baseline_gluon.py:194-209).
+// Common building block (gfx950, wave64): v_mfma_f32_16x16x128_f8f6f4 (OCP
+// e4m3 x e4m3 -> fp32).  One instruction covers a whole 128-K scale group of a
+// 16x16 output block, so each group's product lands in a fresh fp32 register
+// quad that is promoted immediately: acc = fma(p, As[m,g] * Bs[nb,g], acc).
+// Weights sit on the MFMA row side and tokens on the column side (the
+// reference's SWAP_AB orientation, used for every M): a lane's four outputs
+// then share one token and one 128-row weight block, so the promotion factor
+// is ONE fp32 scalar per lane per 16x16 block and group.
+//
+// Operand layout in a lane (both operands identical): row (lane & 15) of a
+// 16-row block, bytes [32 * (lane >> 4), +32) of the 128-byte group.  Since A
+// and B use the same byte -> K assignment, the MFMA reduction covers exactly
+// the 128 products of the group whatever order the hardware sums them in.
+//
+// Kernels:
+//  * fp8bg_tiled  - LDS-tiled workgroup tile (weights x tokens), 4 waves, a
+//                   128-K group staged global -> LDS with 16-byte loads and
+//                   double-buffered; optional cross-workgroup split-K (tail
+//                   wave or full grid) whose fp32 partials are summed by
+//                   fp8bg_split_reduce in fixed split order.
+//  * fp8bg_skinny - small-M kernel: no LDS staging; every wave loads its
+//                   operands straight from global memory into MFMA registers
+//                   and the S waves of a workgroup split the K groups of one
+//                   tile among themselves (deep memory-level parallelism for
+//                   weight streaming); the S partial tiles are summed through
+//                   LDS in fixed wave order.
+//  * fp8bg_split_reduce - fixed-order sum of split-K partials -> bf16.
+// Every reduction order is fixed by the configuration, so results are bitwise
+// reproducible run to run and under hipGraph replay.  No kernel uses atomics,
+// fences beyond workgroup scope, or spin waits.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -49,10 +59,10 @@ struct KArgs {
     const float* As;       // [M, K/128]
     const float* Bs;       // [N/128, K/128]
     uint16_t* C;           // [M, N] bf16, row stride N
-    float* ws;             // split-K partials
-    int* cnt;              // split-K arrival counters
+    float* ws;             // split-K partials [split tile][split][tt][tw]
     int64_t as_sm, as_sk, bs_sn, bs_sk;
     int M, N, K;
+    int tw, tt;            // workgroup tile (weight rows, tokens)
     int tiles_w, tiles_t;
     int n_dp;              // tiles computed whole
     int split;             // workgroups per split tile
@@ -69,11 +79,32 @@ __device__ __forceinline__ uint32_t bf16_bits(float f) {
     return u >> 16;
 }
 
+__device__ __forceinline__ uint2 pack_bf16x4(const f32x4& v) {
+    uint2 o;
+    o.x = bf16_bits(v[0]) | (bf16_bits(v[1]) << 16);
+    o.y = bf16_bits(v[2]) | (bf16_bits(v[3]) << 16);
+    return o;
+}
+
 __device__ __forceinline__ f32x4 mfma16x16x128(const i32x8& w, const i32x8& t) {
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
     // cbsz/blgp format 0 = OCP e4m3 for both operands; scale operands 0 =
     // unscaled instruction.
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, t, zero, 0, 0, 0, 0, 0, 0);
+}
+
+__device__ __forceinline__ void promote(f32x4& acc, const f32x4& p, float s) {
+    acc[0] = __builtin_fmaf(p[0], s, acc[0]);
+    acc[1] = __builtin_fmaf(p[1], s, acc[1]);
+    acc[2] = __builtin_fmaf(p[2], s, acc[2]);
+    acc[3] = __builtin_fmaf(p[3], s, acc[3]);
+}
+
+// 32 operand bytes of one lane: two 16-byte global loads.
+__device__ __forceinline__ i32x8 load_op(const uint8_t* p) {
+    const i32x4 lo = *(const i32x4*)p;
+    const i32x4 hi = *(const i32x4*)(p + 16);
+    return (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
 // Bijective remap of workgroup ids 0..n-1 so that ids dealt to the same XCD
@@ -84,8 +115,25 @@ __device__ __forceinline__ int xcd_remap(int pid, int n) {
     return xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
 }
 
+// Grouped tile order (GROUP_SIZE_M semantics, reference
+// kernels/baseline_triton.py:36-45): runs of group_t token tiles sweep the
+// weight tiles together so their weight rows are reused while cached.
+__device__ __forceinline__ void tile_origin(int tile, const KArgs& a, int& w0, int& t0) {
+    const int per_group = a.group_t * a.tiles_w;
+    const int first_t = (tile / per_group) * a.group_t;
+    const int gsize = min(a.tiles_t - first_t, a.group_t);
+    const int local = tile % per_group;
+    const int pt = first_t + local % gsize;
+    const int pw = local / gsize;
+    w0 = pw * a.tw;
+    t0 = pt * a.tt;
+}
+
+// ===========================================================================
+// LDS-tiled kernel
+// ===========================================================================
 template <int TW, int TT, int WW, int WT, int KF>
-__global__ __launch_bounds__(kThreads) void fp8bg_xdl(KArgs a) {
+__global__ __launch_bounds__(kThreads) void fp8bg_tiled(KArgs a) {
     static_assert(WW * WT == kThreads / 64, "4 waves per workgroup");
     constexpr int WTW = TW / WW;               // weight rows per wave
     constexpr int WTT = TT / WT;               // tokens per wave
@@ -101,14 +149,13 @@ __global__ __launch_bounds__(kThreads) void fp8bg_xdl(KArgs a) {
 
     __shared__ __attribute__((aligned(16))) unsigned char lds[2 * BUF];
     extern __shared__ float s_as[];            // [TT][kcount] when scale_lds
-    __shared__ int s_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wv_w = wave % WW, wv_t = wave / WW;
 
-    // ---- tile decode (reference baseline_gluon.py:109-126) ----
+    // ---- tile decode ----
     const int KG = KF ? KF : (a.K / kGroupK);
     int pid = blockIdx.x;
     int tile, sidx = 0, kcount, k_lo;
@@ -124,15 +171,13 @@ __global__ __launch_bounds__(kThreads) void fp8bg_xdl(KArgs a) {
         kcount = KG / a.split;
         k_lo = sidx * kcount;
     }
-    const int per_group = a.group_t * a.tiles_w;
-    const int first_t = (tile / per_group) * a.group_t;
-    const int gsize = min(a.tiles_t - first_t, a.group_t);
-    const int pt = first_t + (tile % gsize);
-    const int pw = (tile % per_group) / gsize;
-    const int w0 = pw * TW, t0 = pt * TT;
+    int w0, t0;
+    tile_origin(tile, a, w0, t0);
 
     // ---- per-thread global->LDS chunk assignment (fixed across groups) ----
-    // chunk c: row c/8 of the stacked [weights; tokens] tile, 16-byte column c%8.
+    // chunk c: row c/8 of the stacked [weights; tokens] tile, 16-byte column
+    // c%8, stored at column (c%8) ^ (row & 7) so that the operand reads (8
+    // consecutive lanes = 8 consecutive rows, same chunk) hit distinct banks.
     const uint8_t* gptr[NLD];
     int loff[NLD];
 #pragma unroll
@@ -165,7 +210,6 @@ __global__ __launch_bounds__(kThreads) void fp8bg_xdl(KArgs a) {
     };
 
     // ---- scales ----
-    // token of this lane in token block t; weight 128-block of weight block w
     int tok[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) tok[t] = min(t0 + wv_t * WTT + t * 16 + (lane & 15), a.M - 1);
@@ -176,7 +220,8 @@ __global__ __launch_bounds__(kThreads) void fp8bg_xdl(KArgs a) {
 
     if (a.scale_lds) {
         // Stage As[tile tokens, k_lo .. k_lo+kcount) once; walk memory along
-        // whichever As stride is unit so the loads coalesce.
+        // whichever As stride is unit so the loads coalesce
+        // (reference kernels/kernel_scale_tma.py:160-165).
         const int n_el = TT * kcount;
         if (a.as_sk == 1) {
             for (int e = tid; e < n_el; e += kThreads) {
@@ -212,10 +257,6 @@ __global__ __launch_bounds__(kThreads) void fp8bg_xdl(KArgs a) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[w][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    // Operand fetch: lane reads row (lane & 15) of a 16-row block, K bytes
-    // [32*(lane>>4), +32) of the group, as two swizzled 16-byte chunks.  The
-    // same K order is used for both operands, so the MFMA reduction is exact
-    // regardless of how the hardware orders K inside a lane.
     const int c0 = ((lane >> 4) * 2) ^ (lane & 7);
     auto opread = [&](int buf, int row) -> i32x8 {
         const unsigned char* base = lds + buf * BUF + row * kRowBytes;
@@ -252,14 +293,7 @@ __global__ __launch_bounds__(kThreads) void fp8bg_xdl(KArgs a) {
         for (int w = 0; w < NW; ++w) {
             const i32x8 wop = opread(buf, wv_w * WTW + w * 16 + (lane & 15));
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const f32x4 p = mfma16x16x128(wop, top[t]);
-                const float s = sa[t] * sb[w];
-                acc[w][t][0] = __builtin_fmaf(p[0], s, acc[w][t][0]);
-                acc[w][t][1] = __builtin_fmaf(p[1], s, acc[w][t][1]);
-                acc[w][t][2] = __builtin_fmaf(p[2], s, acc[w][t][2]);
-                acc[w][t][3] = __builtin_fmaf(p[3], s, acc[w][t][3]);
-            }
+            for (int t = 0; t < NT; ++t) promote(acc[w][t], mfma16x16x128(wop, top[t]), sa[t] * sb[w]);
         }
         if (more) sstore(buf ^ 1, stage);
         __syncthreads();
@@ -267,8 +301,8 @@ __global__ __launch_bounds__(kThreads) void fp8bg_xdl(KArgs a) {
 
     // ---- epilogue ----
     // Output block (w, t): this lane holds token (lane & 15) and the four
-    // consecutive weight rows 4*(lane >> 4) .. +3 -> one 8-byte bf16 store.
-    auto store_c = [&](const f32x4 (&v)[NW][NT]) {
+    // consecutive weight rows 4*(lane >> 4) .. +3.
+    if (blockIdx.x < a.n_dp) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int m = t0 + wv_t * WTT + t * 16 + (lane & 15);
@@ -277,69 +311,175 @@ __global__ __launch_bounds__(kThreads) void fp8bg_xdl(KArgs a) {
             for (int w = 0; w < NW; ++w) {
                 const int n = w0 + wv_w * WTW + w * 16 + (lane >> 4) * 4;
                 if (n >= a.N) continue;
-                uint2 o;
-                o.x = bf16_bits(v[w][t][0]) | (bf16_bits(v[w][t][1]) << 16);
-                o.y = bf16_bits(v[w][t][2]) | (bf16_bits(v[w][t][3]) << 16);
-                *(uint2*)(a.C + (size_t)m * a.N + n) = o;
+                *(uint2*)(a.C + (size_t)m * a.N + n) = pack_bf16x4(acc[w][t]);
             }
         }
-    };
-
-    if (blockIdx.x < a.n_dp) {
-        store_c(acc);
         return;
     }
+    // Split tile: publish this K range's fp32 partial, row-major [tt][tw]
+    // inside the tile's slab; fp8bg_split_reduce sums the slabs afterwards.
+    float* mine = a.ws + ((size_t)(tile - a.n_dp) * a.split + sidx) * (size_t)(TW * TT);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int tl = wv_t * WTT + t * 16 + (lane & 15);
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const int wl = wv_w * WTW + w * 16 + (lane >> 4) * 4;
+            *(f32x4*)(mine + tl * TW + wl) = acc[w][t];
+        }
+    }
+}
 
-    // Split tile: publish the partial, count arrivals, last one reduces.
-    const int stile = tile - a.n_dp;
-    constexpr int TILE_EL = TW * TT;
-    const int wave_off = wave * (WTW * WTT);
-    float* slab0 = a.ws + (size_t)stile * a.split * TILE_EL + wave_off;
-    {
-        float* mine = slab0 + (size_t)sidx * TILE_EL;
-#pragma unroll
-        for (int w = 0; w < NW; ++w)
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-                *(f32x4*)(mine + ((w * NT + t) * 64 + lane) * 4) = acc[w][t];
+// ===========================================================================
+// Small-M kernel: operands straight from global memory, waves split K
+// ===========================================================================
+template <int NWB, int NTB, int S, int U>
+__global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
+    constexpr int TW = 16 * NWB, TT = 16 * NTB, NB = NWB * NTB;
+    __shared__ f32x4 red[S][NB][64];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, q = lane >> 4;
+
+    // Tokens vary fastest, so the workgroups that share weight rows are
+    // adjacent (and, with xcd_remap, on one XCD's L2).
+    // With a cross-workgroup split (full mode only) workgroup pid computes
+    // K range pid % split of tile pid / split.
+    const int pid = blockIdx.x;
+    int tile = pid, sidx = 0;
+    if (a.split > 1) {
+        tile = pid / a.split;
+        sidx = pid % a.split;
+    } else if (a.xcd_remap) {
+        tile = xcd_remap(pid, a.tiles_w * a.tiles_t);
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const int old = __hip_atomic_fetch_add(a.cnt + stile, 1, __ATOMIC_ACQ_REL,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (old == a.split - 1);
+    const int pt = tile % a.tiles_t, pw = tile / a.tiles_t;
+    const int w0 = pw * TW, t0 = pt * TT;
+
+    const int KG = a.K / kGroupK;
+    const int kcount = KG / a.split;
+    const int k_lo = sidx * kcount;
+
+    const uint8_t* wp[NWB];
+    const float* bsp[NWB];
+#pragma unroll
+    for (int w = 0; w < NWB; ++w) {
+        const int n = min(w0 + 16 * w + r, a.N - 1);
+        wp[w] = a.B + (size_t)n * a.K + 32 * q;
+        bsp[w] = a.Bs + (int64_t)(min(w0 + 16 * w, a.N - 1) >> 7) * a.bs_sn;
     }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    f32x4 tot[NW][NT];
-    for (int s = 0; s < a.split; ++s) {
-        const float* src = slab0 + (size_t)s * TILE_EL;
+    const uint8_t* tp[NTB];
+    const float* asp[NTB];
 #pragma unroll
-        for (int w = 0; w < NW; ++w)
+    for (int t = 0; t < NTB; ++t) {
+        const int m = min(t0 + 16 * t + r, a.M - 1);
+        tp[t] = a.A + (size_t)m * a.K + 32 * q;
+        asp[t] = a.As + (int64_t)m * a.as_sm;
+    }
+
+    f32x4 acc[NWB][NTB];
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const f32x4 v = (s == sidx) ? acc[w][t]
-                                            : *(const f32x4*)(src + ((w * NT + t) * 64 + lane) * 4);
-                if (s == 0)
-                    tot[w][t] = v;
-                else {
-                    tot[w][t][0] += v[0];
-                    tot[w][t][1] += v[1];
-                    tot[w][t][2] += v[2];
-                    tot[w][t][3] += v[3];
+    for (int w = 0; w < NWB; ++w)
+#pragma unroll
+        for (int t = 0; t < NTB; ++t) acc[w][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    // This wave's groups: k_lo + wave + S*j, j = 0 .. J-1.
+    const int J = wave < kcount ? (kcount - 1 - wave) / S + 1 : 0;
+    for (int j0 = 0; j0 < J; j0 += U) {
+        i32x8 wv[U][NWB], tv[U][NTB];
+        float sa[U][NTB], sb[U][NWB];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (j0 + u < J) {
+                const int g = k_lo + wave + S * (j0 + u);
+#pragma unroll
+                for (int w = 0; w < NWB; ++w) {
+                    wv[u][w] = load_op(wp[w] + (size_t)g * kGroupK);
+                    sb[u][w] = bsp[w][(int64_t)g * a.bs_sk];
+                }
+#pragma unroll
+                for (int t = 0; t < NTB; ++t) {
+                    tv[u][t] = load_op(tp[t] + (size_t)g * kGroupK);
+                    sa[u][t] = asp[t][(int64_t)g * a.as_sk];
                 }
             }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (j0 + u < J) {
+#pragma unroll
+                for (int w = 0; w < NWB; ++w)
+#pragma unroll
+                    for (int t = 0; t < NTB; ++t)
+                        promote(acc[w][t], mfma16x16x128(wv[u][w], tv[u][t]), sa[u][t] * sb[u][w]);
+            }
+        }
     }
-    store_c(tot);
-    if (tid == 0) __hip_atomic_store(a.cnt + stile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // Fixed-order sum of the S wave partials through LDS.
+#pragma unroll
+    for (int w = 0; w < NWB; ++w)
+#pragma unroll
+        for (int t = 0; t < NTB; ++t) red[wave][w * NTB + t][lane] = acc[w][t];
+    __syncthreads();
+    for (int b = wave; b < NB; b += S) {
+        f32x4 s = red[0][b][lane];
+#pragma unroll
+        for (int k = 1; k < S; ++k) {
+            const f32x4 v = red[k][b][lane];
+            s[0] += v[0];
+            s[1] += v[1];
+            s[2] += v[2];
+            s[3] += v[3];
+        }
+        const int w = b / NTB, t = b % NTB;
+        const int tl = 16 * t + r, wl = 16 * w + 4 * q;
+        if (a.split > 1) {
+            float* mine = a.ws + ((size_t)tile * a.split + sidx) * (size_t)(TW * TT);
+            *(f32x4*)(mine + tl * TW + wl) = s;
+        } else {
+            const int m = t0 + tl, n = w0 + wl;
+            if (m < a.M && n < a.N) *(uint2*)(a.C + (size_t)m * a.N + n) = pack_bf16x4(s);
+        }
+    }
+}
+
+// ===========================================================================
+// Split-K reduction: one workgroup per split tile, fixed split order.
+// ===========================================================================
+__global__ __launch_bounds__(kThreads) void fp8bg_split_reduce(KArgs a, int skinny_order) {
+    const int stile = blockIdx.x;
+    int w0, t0;
+    if (skinny_order) {
+        w0 = (stile / a.tiles_t) * a.tw;
+        t0 = (stile % a.tiles_t) * a.tt;
+    } else {
+        tile_origin(a.n_dp + stile, a, w0, t0);
+    }
+    const int tile_el = a.tw * a.tt;
+    const float* base = a.ws + (size_t)stile * a.split * tile_el;
+    for (int e = threadIdx.x * 4; e < tile_el; e += kThreads * 4) {
+        const int tl = e / a.tw, wl = e % a.tw;
+        const int m = t0 + tl, n = w0 + wl;
+        if (m >= a.M || n >= a.N) continue;
+        f32x4 s = *(const f32x4*)(base + e);
+        for (int k = 1; k < a.split; ++k) {
+            const f32x4 v = *(const f32x4*)(base + (size_t)k * tile_el + e);
+            s[0] += v[0];
+            s[1] += v[1];
+            s[2] += v[2];
+            s[3] += v[3];
+        }
+        *(uint2*)(a.C + (size_t)m * a.N + n) = pack_bf16x4(s);
+    }
 }
 
 // ---------------------------------------------------------------------------
-// Compiled instances: (block_w, block_t, waves_w, waves_t, k_fixed)
+// Compiled instances
 // ---------------------------------------------------------------------------
-#define FP8BG_INSTANCES(X)                                                     \
+// tiled: (block_w, block_t, waves_w, waves_t, k_fixed)
+#define FP8BG_TILED(X)                                                         \
     X(64, 16, 4, 1, 0) X(128, 16, 4, 1, 0) X(256, 16, 4, 1, 0)                 \
     X(64, 32, 4, 1, 0) X(128, 32, 4, 1, 0) X(256, 32, 4, 1, 0)                 \
     X(64, 64, 4, 1, 0) X(128, 64, 4, 1, 0) X(256, 64, 4, 1, 0)                 \
@@ -349,29 +489,57 @@ __global__ __launch_bounds__(kThreads) void fp8bg_xdl(KArgs a) {
     X(128, 32, 4, 1, 2) X(128, 64, 4, 1, 2) X(128, 128, 2, 2, 2)               \
     X(256, 128, 4, 1, 2)
 
+// skinny: (weight 16-blocks, token 16-blocks, waves splitting K, groups in flight)
+#define FP8BG_SKINNY(X)                                                        \
+    X(1, 1, 4, 1) X(1, 1, 4, 2) X(1, 1, 8, 1) X(1, 1, 8, 2) X(1, 1, 8, 4)      \
+    X(2, 1, 4, 1) X(2, 1, 4, 2) X(2, 1, 8, 1) X(2, 1, 8, 2) X(2, 1, 8, 4)      \
+    X(4, 1, 4, 1) X(4, 1, 4, 2) X(4, 1, 8, 1) X(4, 1, 8, 2) X(4, 1, 8, 4)      \
+    X(1, 2, 4, 2) X(1, 2, 8, 1) X(1, 2, 8, 2)                                  \
+    X(2, 2, 4, 2) X(2, 2, 8, 1) X(2, 2, 8, 2)                                  \
+    X(4, 2, 4, 2) X(4, 2, 8, 1) X(4, 2, 8, 2)                                  \
+    X(1, 4, 4, 2) X(1, 4, 8, 1) X(1, 4, 8, 2)                                  \
+    X(2, 4, 4, 2) X(2, 4, 8, 1) X(2, 4, 8, 2)                                  \
+    X(4, 4, 4, 1) X(4, 4, 8, 1) X(4, 4, 4, 2)
+
 struct Instance {
-    int tw, tt, ww, wt, kf;
+    int kind, tw, tt, ww, wt, wk, unroll, kf, threads;
     void (*launch)(dim3 grid, size_t shm, hipStream_t s, const KArgs& a);
 };
 
-#define FP8BG_LAUNCHER(TW, TT, WW, WT, KF)                                                   \
-    static void launch_##TW##_##TT##_##WW##_##WT##_##KF(dim3 g, size_t shm, hipStream_t s,  \
-                                                        const KArgs& a) {                   \
-        hipLaunchKernelGGL((fp8bg_xdl<TW, TT, WW, WT, KF>), g, dim3(kThreads), shm, s, a);  \
+#define FP8BG_TILED_LAUNCHER(TW, TT, WW, WT, KF)                                             \
+    static void tiled_##TW##_##TT##_##WW##_##WT##_##KF(dim3 g, size_t shm, hipStream_t s,   \
+                                                       const KArgs& a) {                    \
+        hipLaunchKernelGGL((fp8bg_tiled<TW, TT, WW, WT, KF>), g, dim3(kThreads), shm, s, a); \
     }
-FP8BG_INSTANCES(FP8BG_LAUNCHER)
-#undef FP8BG_LAUNCHER
+FP8BG_TILED(FP8BG_TILED_LAUNCHER)
+#undef FP8BG_TILED_LAUNCHER
 
-#define FP8BG_ENTRY(TW, TT, WW, WT, KF) {TW, TT, WW, WT, KF, launch_##TW##_##TT##_##WW##_##WT##_##KF},
-const Instance kInstances[] = {FP8BG_INSTANCES(FP8BG_ENTRY)};
-#undef FP8BG_ENTRY
+#define FP8BG_SKINNY_LAUNCHER(NW, NT, S, U)                                                  \
+    static void skinny_##NW##_##NT##_##S##_##U(dim3 g, size_t shm, hipStream_t s,           \
+                                               const KArgs& a) {                            \
+        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U>), g, dim3(64 * S), shm, s, a);        \
+    }
+FP8BG_SKINNY(FP8BG_SKINNY_LAUNCHER)
+#undef FP8BG_SKINNY_LAUNCHER
+
+#define FP8BG_TILED_ENTRY(TW, TT, WW, WT, KF) \
+    {FP8BG_KIND_TILED, TW, TT, WW, WT, 1, 1, KF, kThreads, tiled_##TW##_##TT##_##WW##_##WT##_##KF},
+#define FP8BG_SKINNY_ENTRY(NW, NT, S, U) \
+    {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 0, 64 * S, skinny_##NW##_##NT##_##S##_##U},
+const Instance kInstances[] = {FP8BG_TILED(FP8BG_TILED_ENTRY) FP8BG_SKINNY(FP8BG_SKINNY_ENTRY)};
+#undef FP8BG_TILED_ENTRY
+#undef FP8BG_SKINNY_ENTRY
 constexpr int kNumInstances = sizeof(kInstances) / sizeof(kInstances[0]);
 
 int find_instance(const fp8bg_config* c) {
     for (int i = 0; i < kNumInstances; ++i) {
         const Instance& k = kInstances[i];
-        if (k.tw == c->block_w && k.tt == c->block_t && k.ww == c->waves_w &&
-            k.wt == c->waves_t && k.kf == c->k_fixed)
+        if (k.kind != c->kind || k.tw != c->block_w || k.tt != c->block_t) continue;
+        if (k.kind == FP8BG_KIND_TILED && k.ww == c->waves_w && k.wt == c->waves_t &&
+            k.kf == c->k_fixed)
+            return i;
+        if (k.kind == FP8BG_KIND_SKINNY && k.wk == c->waves_k && k.unroll == c->unroll &&
+            c->k_fixed == 0)
             return i;
     }
     return -1;
@@ -381,14 +549,14 @@ int find_instance(const fp8bg_config* c) {
 
 extern "C" {
 
-int fp8bg_version(void) { return 1; }
+int fp8bg_version(void) { return FP8BG_ABI_VERSION; }
 
 const char* fp8bg_strerror(int code) {
     switch (code) {
         case FP8BG_OK: return "ok";
         case FP8BG_ERR_SHAPE: return "invalid shape: need M>=1 and N, K positive multiples of 128";
         case FP8BG_ERR_CONFIG: return "invalid or uncompiled kernel configuration";
-        case FP8BG_ERR_WORKSPACE: return "split-K workspace or counters missing or too small";
+        case FP8BG_ERR_WORKSPACE: return "split-K workspace missing or too small";
         case FP8BG_ERR_ALIGN: return "A, B and C must be 16-byte aligned";
         case FP8BG_ERR_LAUNCH: return "HIP kernel launch failed";
         case FP8BG_ERR_DEVICE: return "HIP device query failed";
@@ -422,9 +590,12 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     const int kg = K / 128;
     const Instance& k = kInstances[ki];
     if (k.kf && kg != k.kf) return FP8BG_ERR_CONFIG;
+    const bool skinny = k.kind == FP8BG_KIND_SKINNY;
+    if (skinny && (cfg->flags & FP8BG_FLAG_SCALE_LDS)) return FP8BG_ERR_CONFIG;
 
     int split = (cfg->split_mode == FP8BG_SPLIT_NONE || k.kf) ? 1 : cfg->split;
     if (kg % split) split = 1;  // reference baseline_gluon.py:274-276
+    if (skinny && split > 1 && cfg->split_mode != FP8BG_SPLIT_FULL) return FP8BG_ERR_CONFIG;
     const int64_t tiles_w = (N + k.tw - 1) / k.tw;
     const int64_t tiles_t = ((int64_t)M + k.tt - 1) / k.tt;
     const int64_t tiles = tiles_w * tiles_t;
@@ -434,8 +605,13 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     const int64_t n_dp = tiles - n_split;
     const int64_t grid = n_dp + n_split * split;
     if (grid > 0x7fffffff) return FP8BG_ERR_SHAPE;
-    int64_t lds = 2LL * (k.tw + k.tt) * 128;
-    if (cfg->flags & FP8BG_FLAG_SCALE_LDS) lds += (int64_t)k.tt * kg * 4;
+    int64_t lds;
+    if (skinny) {
+        lds = (int64_t)k.wk * (k.tw / 16) * (k.tt / 16) * 64 * 16;
+    } else {
+        lds = 2LL * (k.tw + k.tt) * 128;
+        if (cfg->flags & FP8BG_FLAG_SCALE_LDS) lds += (int64_t)k.tt * kg * 4;
+    }
     if (lds > kMaxLds) return FP8BG_ERR_CONFIG;
 
     plan->tiles_w = (int32_t)tiles_w;
@@ -445,9 +621,10 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     plan->n_dp = (int32_t)n_dp;
     plan->n_split = (int32_t)n_split;
     plan->grid = (int32_t)grid;
-    plan->cnt_elems = (int32_t)n_split;
+    plan->launches = n_split ? 2 : 1;
     plan->ws_elems = n_split * split * (int64_t)k.tw * k.tt;
     plan->lds_bytes = (int32_t)lds;
+    plan->threads = k.threads;
     plan->kernel_id = ki;
     return FP8BG_OK;
 }
@@ -455,16 +632,16 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
 int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_m,
                int64_t as_stride_k, const float* Bs, int64_t bs_stride_n, int64_t bs_stride_k,
                void* C, int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg,
-               int32_t num_cus, float* ws, int64_t ws_elems, int32_t* cnt, int32_t cnt_elems,
-               void* stream) {
+               int32_t num_cus, float* ws, int64_t ws_elems, void* stream) {
     if (!A || !B || !As || !Bs || !C) return FP8BG_ERR_NULL;
     fp8bg_plan p;
     const int rc = fp8bg_make_plan(M, N, K, cfg, num_cus, &p);
     if (rc != FP8BG_OK) return rc;
     if ((((uintptr_t)A) | ((uintptr_t)B) | ((uintptr_t)C)) & 15) return FP8BG_ERR_ALIGN;
-    if (p.n_split > 0 && (!ws || !cnt || ws_elems < p.ws_elems || cnt_elems < p.cnt_elems))
+    if (p.n_split > 0 && (!ws || ws_elems < p.ws_elems || (((uintptr_t)ws) & 15)))
         return FP8BG_ERR_WORKSPACE;
 
+    const Instance& k = kInstances[p.kernel_id];
     KArgs a;
     a.A = (const uint8_t*)A;
     a.B = (const uint8_t*)B;
@@ -472,7 +649,6 @@ int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_
     a.Bs = Bs;
     a.C = (uint16_t*)C;
     a.ws = ws;
-    a.cnt = cnt;
     a.as_sm = as_stride_m;
     a.as_sk = as_stride_k;
     a.bs_sn = bs_stride_n;
@@ -480,6 +656,8 @@ int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_
     a.M = M;
     a.N = N;
     a.K = K;
+    a.tw = k.tw;
+    a.tt = k.tt;
     a.tiles_w = p.tiles_w;
     a.tiles_t = p.tiles_t;
     a.n_dp = p.n_dp;
@@ -487,10 +665,16 @@ int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_
     a.group_t = cfg->group_t;
     a.xcd_remap = (cfg->flags & FP8BG_FLAG_XCD_REMAP) ? 1 : 0;
     a.scale_lds = (cfg->flags & FP8BG_FLAG_SCALE_LDS) ? 1 : 0;
-    const Instance& k = kInstances[p.kernel_id];
     const size_t shm = a.scale_lds ? (size_t)k.tt * (K / 128) * sizeof(float) : 0;
-    k.launch(dim3(p.grid), shm, (hipStream_t)stream, a);
-    return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
+    hipStream_t s = (hipStream_t)stream;
+    k.launch(dim3(p.grid), shm, s, a);
+    if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
+    if (p.n_split > 0) {
+        hipLaunchKernelGGL(fp8bg_split_reduce, dim3(p.n_split), dim3(kThreads), 0, s, a,
+                           k.kind == FP8BG_KIND_SKINNY ? 1 : 0);
+        if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
+    }
+    return FP8BG_OK;
 }
 
 }  // extern "C"

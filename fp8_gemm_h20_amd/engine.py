@@ -5,7 +5,8 @@ so importing the package and selecting configs neither loads libfp8bg.so nor
 touches the GPU.  `run(entry, args)` calls fn(A, B, As, Bs, dict(config)).
 
 gfx950-native impls written by this package's tables:
-  xdl     LDS-tiled MFMA kernel, tail or full split-K
+  tiled   LDS-tiled MFMA kernel, optional tail or full split-K
+  skinny  small-M kernel: operands straight to registers, waves split K
   shortk  K == 256 kernel, no K loop (also accepts the reference's BM/BN keys)
 Reference H20 impl names, accepted so reference tables keep working; each
 runs on the gfx950 kernels (see kernels.py):
@@ -15,7 +16,8 @@ from functools import lru_cache
 from importlib import import_module
 
 KERNELS = {
-    "xdl": ("kernels", "xdl"),
+    "tiled": ("kernels", "tiled"),
+    "skinny": ("kernels", "skinny"),
     "shortk": ("kernels", "shortk"),
     "triton": ("kernels", "triton"),
     "gluon": ("kernels", "gluon"),
@@ -24,7 +26,7 @@ KERNELS = {
 }
 
 # impls whose config uses this package's gfx950 keys
-NATIVE = ("xdl", "shortk")
+NATIVE = ("tiled", "skinny", "shortk")
 
 
 @lru_cache(maxsize=None)

@@ -3,15 +3,18 @@
 Each function keeps the reference's L0 wrapper contract
 (fp8_gemm_h20/engine.py:18-19): A[M,K], B[N,K] contiguous e4m3fn CUDA tensors,
 As[M,K/128] and Bs[N/128,K/128] fp32 with any strides, `config` a plain dict;
-it allocates C = empty(M, N, bf16) on A's device, enqueues one HIP kernel on
-the current stream through the C ABI (include/fp8bg.h) and returns C without
-synchronising.
+it allocates C = empty(M, N, bf16) on A's device, enqueues the HIP kernel(s)
+on the current stream through the C ABI (include/fp8bg.h) and returns C
+without synchronising.
 
 Two families of config dicts are accepted:
 
-* gfx950-native entries (impl "xdl", "shortk") written by this package's
-  tuner: BLOCK_W, BLOCK_T, WAVES_W, WAVES_T, SPLIT, SPLIT_MODE,
-  GROUP_SIZE_M, SCALE_LDS, XCD_REMAP.
+* gfx950-native entries written by this package's tuner:
+  - impl "tiled": BLOCK_W, BLOCK_T, WAVES_W, WAVES_T, SPLIT, SPLIT_MODE,
+    GROUP_SIZE_M, SCALE_LDS, XCD_REMAP (LDS-tiled kernel);
+  - impl "skinny": BLOCK_W, BLOCK_T, WAVES_K, UNROLL, SPLIT, SPLIT_MODE,
+    XCD_REMAP (small-M kernel, waves split K);
+  - impl "shortk": BLOCK_W, BLOCK_T (K == 256, no K loop).
 * the reference's H20 entries (impl "triton", "gluon", "v2", "scale_tma",
   "shortk" with BM/BN keys), translated onto the nearest compiled gfx950 tile
   so that an existing reference profile table still runs unchanged.
@@ -21,9 +24,10 @@ from functools import lru_cache
 
 from . import _lib
 
-# (block_w, block_t, waves_w, waves_t, k_fixed) compiled into libfp8bg.so;
-# must equal FP8BG_INSTANCES in csrc/fp8bg.hip (checked by tests).
-INSTANCES = (
+# Compiled kernel instances; must equal FP8BG_TILED / FP8BG_SKINNY in
+# csrc/fp8bg.hip (checked by tests).
+# tiled: (block_w, block_t, waves_w, waves_t, k_fixed)
+TILED = (
     (64, 16, 4, 1, 0), (128, 16, 4, 1, 0), (256, 16, 4, 1, 0),
     (64, 32, 4, 1, 0), (128, 32, 4, 1, 0), (256, 32, 4, 1, 0),
     (64, 64, 4, 1, 0), (128, 64, 4, 1, 0), (256, 64, 4, 1, 0),
@@ -33,33 +37,48 @@ INSTANCES = (
     (128, 32, 4, 1, 2), (128, 64, 4, 1, 2), (128, 128, 2, 2, 2),
     (256, 128, 4, 1, 2),
 )
+# skinny: (16-row weight blocks, 16-token blocks, waves_k, unroll)
+SKINNY = (
+    (1, 1, 4, 1), (1, 1, 4, 2), (1, 1, 8, 1), (1, 1, 8, 2), (1, 1, 8, 4),
+    (2, 1, 4, 1), (2, 1, 4, 2), (2, 1, 8, 1), (2, 1, 8, 2), (2, 1, 8, 4),
+    (4, 1, 4, 1), (4, 1, 4, 2), (4, 1, 8, 1), (4, 1, 8, 2), (4, 1, 8, 4),
+    (1, 2, 4, 2), (1, 2, 8, 1), (1, 2, 8, 2),
+    (2, 2, 4, 2), (2, 2, 8, 1), (2, 2, 8, 2),
+    (4, 2, 4, 2), (4, 2, 8, 1), (4, 2, 8, 2),
+    (1, 4, 4, 2), (1, 4, 8, 1), (1, 4, 8, 2),
+    (2, 4, 4, 2), (2, 4, 8, 1), (2, 4, 8, 2),
+    (4, 4, 4, 1), (4, 4, 8, 1), (4, 4, 4, 2),
+)
+# skinny instances as (block_w, block_t, waves_k, unroll)
+SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
+# back-compat name used by tests and the tuner
+INSTANCES = TILED
 
 SPLIT_MODES = {"none": _lib.SPLIT_NONE, "tail": _lib.SPLIT_TAIL, "full": _lib.SPLIT_FULL}
-TILE_W = (64, 128, 256)
-TILE_T = (16, 32, 64, 128, 256)
 
 
 def default_waves(block_w, block_t, k_fixed=0):
-    """Wave grid of the first compiled instance with this tile."""
-    for tw, tt, ww, wt, kf in INSTANCES:
+    """Wave grid of the first compiled tiled instance with this tile."""
+    for tw, tt, ww, wt, kf in TILED:
         if (tw, tt, kf) == (block_w, block_t, k_fixed):
             return ww, wt
     return None
 
 
 def is_compiled(block_w, block_t, waves_w, waves_t, k_fixed=0):
-    return (block_w, block_t, waves_w, waves_t, k_fixed) in INSTANCES
+    return (block_w, block_t, waves_w, waves_t, k_fixed) in TILED
 
 
 def nearest_tile(block_w, block_t, k_fixed=0):
-    """Closest compiled (block_w, block_t) for a requested tile.
+    """Closest compiled tiled (block_w, block_t) for a requested tile.
 
     Used to run reference (H20) table entries: their tiles (16..64 wide)
-    are sized for 78 SMs and warp-level wgmma; gfx950 tiles start at 64 weight
-    rows.  Preference: keep the token tile, then the nearest weight tile.
+    are sized for 78 SMs and warp-level wgmma; gfx950 tiled kernels start at
+    64 weight rows.  Preference: keep the token tile, then the nearest weight
+    tile.
     """
     best = None
-    for tw, tt, _, _, kf in INSTANCES:
+    for tw, tt, _, _, kf in TILED:
         if kf != k_fixed:
             continue
         cost = (abs((tt or 1).bit_length() - max(block_t, 1).bit_length()) * 4
@@ -69,8 +88,24 @@ def nearest_tile(block_w, block_t, k_fixed=0):
     return best[1], best[2]
 
 
-def native_struct(cfg, k_fixed=0):
-    """Build the C config struct from a gfx950-native config dict."""
+def _flags(cfg):
+    flags = 0
+    if cfg.get("SCALE_LDS", False):
+        flags |= _lib.FLAG_SCALE_LDS
+    if cfg.get("XCD_REMAP", False):
+        flags |= _lib.FLAG_XCD_REMAP
+    return flags
+
+
+def _split_mode(cfg, default):
+    mode = cfg.get("SPLIT_MODE", default)
+    if mode not in SPLIT_MODES:
+        raise ValueError(f"SPLIT_MODE must be one of {tuple(SPLIT_MODES)}")
+    return SPLIT_MODES[mode]
+
+
+def tiled_struct(cfg, k_fixed=0):
+    """C config struct for a tiled (or shortk) config dict."""
     tw, tt = int(cfg["BLOCK_W"]), int(cfg["BLOCK_T"])
     ww, wt = cfg.get("WAVES_W"), cfg.get("WAVES_T")
     if ww is None or wt is None:
@@ -78,35 +113,36 @@ def native_struct(cfg, k_fixed=0):
         if waves is None:
             raise ValueError(f"no compiled gfx950 kernel for tile {tw}x{tt} (k_fixed={k_fixed})")
         ww, wt = waves
-    mode = cfg.get("SPLIT_MODE", "full")
-    if mode not in SPLIT_MODES:
-        raise ValueError(f"SPLIT_MODE must be one of {tuple(SPLIT_MODES)}")
-    flags = 0
-    if cfg.get("SCALE_LDS", False):
-        flags |= _lib.FLAG_SCALE_LDS
-    if cfg.get("XCD_REMAP", False):
-        flags |= _lib.FLAG_XCD_REMAP
-    return _lib.Config(tw, tt, int(ww), int(wt), int(cfg.get("SPLIT", 1)), SPLIT_MODES[mode],
-                       int(cfg.get("GROUP_SIZE_M", 1)), flags, k_fixed)
+    return _lib.Config(_lib.KIND_TILED, tw, tt, int(ww), int(wt), 1, 1, int(cfg.get("SPLIT", 1)),
+                       _split_mode(cfg, "full"), int(cfg.get("GROUP_SIZE_M", 1)), _flags(cfg), k_fixed)
+
+
+def skinny_struct(cfg):
+    """C config struct for a skinny config dict."""
+    return _lib.Config(_lib.KIND_SKINNY, int(cfg["BLOCK_W"]), int(cfg["BLOCK_T"]), 1, 1,
+                       int(cfg.get("WAVES_K", 8)), int(cfg.get("UNROLL", 1)),
+                       int(cfg.get("SPLIT", 1)), _split_mode(cfg, "none"), 1, _flags(cfg), 0)
+
+
+# back-compat alias
+native_struct = tiled_struct
 
 
 # ---------------------------------------------------------------------------
-# device state: CU count and split-K buffers
+# device state: CU count and split-K workspaces
 # ---------------------------------------------------------------------------
 _NUM_CUS = {}
 
 
 class SplitBuffers:
-    """Split-K workspace (fp32) and arrival counters (int32) of one
-    (device, stream) pair (reference baseline_gluon.py:229-244).
+    """Split-K workspace (fp32) of one (device, stream) pair (reference
+    baseline_gluon.py:229-244).
 
     Launches on one stream are ordered, so every split-K GEMM on that stream
     can share one workspace; kernels on different streams never share.
-    Counters start at zero and every kernel leaves them zero, so captured
-    hipGraphs can be replayed.
 
     Growth never frees a buffer: a hipGraph captured earlier holds the old
-    device addresses, and torch.cuda.graph() empties the allocator cache at
+    device address, and torch.cuda.graph() empties the allocator cache at
     every capture, which would hand freed blocks back to the driver and leave
     such a graph writing to unmapped memory.  Replaced buffers are therefore
     retired (kept alive until the process ends); sizes at least double on each
@@ -114,27 +150,20 @@ class SplitBuffers:
     """
 
     MIN_WS = 1 << 20
-    MIN_CNT = 4096
 
     def __init__(self, device):
         self.device = device
         self.ws = None
-        self.cnt = None
         self.retired = []
 
-    def get(self, ws_elems, cnt_elems):
+    def get(self, ws_elems):
         import torch
         if self.ws is None or self.ws.numel() < ws_elems:
             size = max(ws_elems, self.MIN_WS, 2 * (self.ws.numel() if self.ws is not None else 0))
             if self.ws is not None:
                 self.retired.append(self.ws)
             self.ws = torch.empty(size, device=self.device, dtype=torch.float32)
-        if self.cnt is None or self.cnt.numel() < cnt_elems:
-            size = max(cnt_elems, self.MIN_CNT, 2 * (self.cnt.numel() if self.cnt is not None else 0))
-            if self.cnt is not None:
-                self.retired.append(self.cnt)
-            self.cnt = torch.zeros(size, device=self.device, dtype=torch.int32)
-        return self.ws, self.cnt
+        return self.ws
 
 
 # (device index, stream handle) -> SplitBuffers
@@ -154,17 +183,17 @@ def num_cus(dev):
     return n
 
 
-def _bufs(dev, ws_elems, cnt_elems):
+def _workspace(dev, ws_elems):
     import torch
     key = (_device_index(dev), torch.cuda.current_stream(dev).cuda_stream)
     bufs = _BUFS.get(key)
     if bufs is None:
         bufs = _BUFS[key] = SplitBuffers(dev)
-    return bufs.get(ws_elems, cnt_elems)
+    return bufs.get(ws_elems)
 
 
 def launch(A, B, As, Bs, cstruct):
-    """Allocate C and enqueue the kernel described by `cstruct`."""
+    """Allocate C and enqueue the kernel(s) described by `cstruct`."""
     import torch
     M, K = A.shape
     N = B.shape[0]
@@ -172,36 +201,45 @@ def launch(A, B, As, Bs, cstruct):
     cus = num_cus(dev)
     plan = _lib.make_plan(M, N, K, cstruct, cus)
     C = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
-    ws_ptr = cnt_ptr = None
-    ws_n = cnt_n = 0
+    ws_ptr, ws_n = None, 0
     if plan.n_split:
-        ws, cnt = _bufs(dev, plan.ws_elems, plan.cnt_elems)
-        ws_ptr, cnt_ptr, ws_n, cnt_n = ws.data_ptr(), cnt.data_ptr(), ws.numel(), cnt.numel()
+        ws = _workspace(dev, plan.ws_elems)
+        ws_ptr, ws_n = ws.data_ptr(), ws.numel()
     stream = torch.cuda.current_stream(dev).cuda_stream
     _lib.check(_lib.lib().fp8bg_gemm(
         A.data_ptr(), B.data_ptr(),
         As.data_ptr(), As.stride(0), As.stride(1),
         Bs.data_ptr(), Bs.stride(0), Bs.stride(1),
         C.data_ptr(), M, N, K, ctypes.byref(cstruct), cus,
-        ws_ptr, ws_n, cnt_ptr, cnt_n, stream))
+        ws_ptr, ws_n, stream))
     return C
-
-
-@lru_cache(maxsize=1024)
-def _native_cached(items, k_fixed):
-    return native_struct(dict(items), k_fixed)
 
 
 def _freeze(config):
     return tuple(sorted(config.items()))
 
 
+@lru_cache(maxsize=1024)
+def _tiled_cached(items, k_fixed):
+    return tiled_struct(dict(items), k_fixed)
+
+
+@lru_cache(maxsize=1024)
+def _skinny_cached(items):
+    return skinny_struct(dict(items))
+
+
 # ---------------------------------------------------------------------------
 # gfx950-native impls
 # ---------------------------------------------------------------------------
-def xdl(A, B, As, Bs, config):
+def tiled(A, B, As, Bs, config):
     """LDS-tiled MFMA kernel with optional tail/full split-K."""
-    return launch(A, B, As, Bs, _native_cached(_freeze(config), 0))
+    return launch(A, B, As, Bs, _tiled_cached(_freeze(config), 0))
+
+
+def skinny(A, B, As, Bs, config):
+    """Small-M kernel: operands straight to registers, waves split K."""
+    return launch(A, B, As, Bs, _skinny_cached(_freeze(config)))
 
 
 def shortk(A, B, As, Bs, config):
@@ -215,7 +253,11 @@ def shortk(A, B, As, Bs, config):
     if "BLOCK_W" not in config:
         tw, tt = nearest_tile(int(config["BN"]), int(config["BM"]), k_fixed=2)
         config = {"BLOCK_W": tw, "BLOCK_T": tt, "GROUP_SIZE_M": int(config.get("GROUP", 1))}
-    return launch(A, B, As, Bs, _native_cached(_freeze(config), 2))
+    return launch(A, B, As, Bs, _tiled_cached(_freeze(config), 2))
+
+
+# earlier name of the tiled impl
+xdl = tiled
 
 
 # ---------------------------------------------------------------------------
@@ -225,7 +267,7 @@ def _compat(tw_req, tt_req, split, mode, group, scale_lds=False):
     tw, tt = nearest_tile(tw_req, tt_req)
     cfg = {"BLOCK_W": tw, "BLOCK_T": tt, "SPLIT": int(split), "SPLIT_MODE": mode,
            "GROUP_SIZE_M": int(group), "SCALE_LDS": bool(scale_lds)}
-    return _native_cached(_freeze(cfg), 0)
+    return _tiled_cached(_freeze(cfg), 0)
 
 
 def triton(A, B, As, Bs, config):

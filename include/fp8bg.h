@@ -32,27 +32,46 @@ extern "C" {
 #define FP8BG_OK             0
 #define FP8BG_ERR_SHAPE      1  /* M<1, N or K not a positive multiple of 128, ... */
 #define FP8BG_ERR_CONFIG     2  /* tile/wave/split combination not built or invalid */
-#define FP8BG_ERR_WORKSPACE  3  /* split-K workspace or counters missing/too small */
+#define FP8BG_ERR_WORKSPACE  3  /* split-K workspace missing, misaligned or too small */
 #define FP8BG_ERR_ALIGN      4  /* A, B or C not 16-byte aligned */
 #define FP8BG_ERR_LAUNCH     5  /* hipLaunchKernel / hip runtime error */
 #define FP8BG_ERR_DEVICE     6  /* device query failed */
 #define FP8BG_ERR_NULL       7  /* required pointer argument is NULL */
 
+/* ABI version returned by fp8bg_version(); bumped on any signature or struct
+ * change. */
+#define FP8BG_ABI_VERSION 2
+
+/* ---- kernel kinds --------------------------------------------------------- */
+/* LDS-tiled kernel: a block_w x block_t workgroup tile, 4 waves in a
+ * waves_w x waves_t grid, each 128-K group staged in LDS (double-buffered).
+ * Replaces the reference's tiled kernels (kernels/baseline_triton.py:28-81,
+ * kernels/baseline_gluon.py:94-211, kernels/kernel_v2.py:94-291). */
+#define FP8BG_KIND_TILED  0
+/* Small-M kernel: no LDS staging; waves_k waves (4 or 8) split the K groups
+ * of one block_w x block_t tile, `unroll` groups in flight per wave, partials
+ * summed in fixed wave order.  The reference's SWAP_AB small-M role
+ * (kernels/baseline_gluon.py:77-83). */
+#define FP8BG_KIND_SKINNY 1
+
 /* ---- split-K modes ------------------------------------------------------ */
-/* No split: every tile runs the full K range (config SPLIT ignored). */
+/* No split: every tile runs the full K range (config split ignored). */
 #define FP8BG_SPLIT_NONE 0
 /* Tail split (reference kernels/baseline_gluon.py:274-287): the first
  * tiles - (tiles % num_cus) tiles run whole; only the last partial wave is
- * split over `split` workgroups whose fp32 partials are summed in fixed
- * split order by the last-arriving workgroup. */
+ * split over `split` workgroups.  Tiled kernel only. */
 #define FP8BG_SPLIT_TAIL 1
 /* Full split (reference kernels/baseline_triton.py:100-114): every tile is
- * split; same deterministic fixed-order in-kernel reduction. */
+ * split. */
 #define FP8BG_SPLIT_FULL 2
+/* In both split modes the fp32 partials go to the caller's workspace and a
+ * second kernel on the same stream sums them in fixed split order and writes
+ * bf16 (deterministic, replay-safe, no atomics or counters). */
 
 /* ---- config flags --------------------------------------------------------- */
 /* Stage the tile's activation scales As[tile rows, k range] in LDS once per
- * workgroup (reference kernels/kernel_scale_tma.py:160-165); any As strides. */
+ * workgroup (reference kernels/kernel_scale_tma.py:160-165); any As strides.
+ * Tiled kernel only. */
 #define FP8BG_FLAG_SCALE_LDS 0x1
 /* Remap workgroup ids so that consecutive tiles run on the same XCD (L2). */
 #define FP8BG_FLAG_XCD_REMAP 0x2
@@ -62,18 +81,22 @@ extern "C" {
  * Replaces the reference's per-entry `config` dict (fp8_gemm_h20/config.py:80-91).
  */
 typedef struct fp8bg_config {
-    int32_t block_w;    /* weight rows (N) per workgroup tile: 64, 128 or 256 */
-    int32_t block_t;    /* tokens (M) per workgroup tile: 16 .. 256, power of 2 */
-    int32_t waves_w;    /* waves along N inside the tile (waves_w*waves_t == 4) */
-    int32_t waves_t;    /* waves along M inside the tile */
-    int32_t split;      /* K split factor, in 128-K groups; normalised to 1 when
-                           it does not divide K/128 (baseline_gluon.py:274-276) */
-    int32_t split_mode; /* FP8BG_SPLIT_* */
-    int32_t group_t;    /* token-tile swizzle group (GROUP_SIZE_M semantics,
-                           baseline_triton.py:36-45); >= 1 */
+    int32_t kind;       /* FP8BG_KIND_* */
+    int32_t block_w;    /* weight rows (N) per workgroup tile */
+    int32_t block_t;    /* tokens (M) per workgroup tile */
+    int32_t waves_w;    /* tiled: waves along N inside the tile (waves_w*waves_t == 4) */
+    int32_t waves_t;    /* tiled: waves along M inside the tile */
+    int32_t waves_k;    /* skinny: waves splitting K inside a workgroup (4 or 8) */
+    int32_t unroll;     /* skinny: 128-K groups in flight per wave */
+    int32_t split;      /* cross-workgroup K split factor, in 128-K groups;
+                           normalised to 1 when it does not divide K/128
+                           (baseline_gluon.py:274-276) */
+    int32_t split_mode; /* FP8BG_SPLIT_* (skinny: NONE or FULL) */
+    int32_t group_t;    /* tiled: token-tile swizzle group (GROUP_SIZE_M
+                           semantics, baseline_triton.py:36-45); >= 1 */
     int32_t flags;      /* FP8BG_FLAG_* */
-    int32_t k_fixed;    /* 0 = runtime K loop; 2 = K==256 short-K kernel with no
-                           K loop (reference kernels/kernel_shortk.py:11-54) */
+    int32_t k_fixed;    /* tiled: 0 = runtime K loop; 2 = K==256 short-K kernel
+                           with no K loop (reference kernels/kernel_shortk.py:11-54) */
 } fp8bg_config;
 
 /*
@@ -89,14 +112,15 @@ typedef struct fp8bg_plan {
     int32_t split;      /* effective split (1 when not split) */
     int32_t n_dp;       /* tiles computed whole (no reduction) */
     int32_t n_split;    /* tiles split over `split` workgroups */
-    int32_t grid;       /* workgroups launched = n_dp + n_split * split */
-    int32_t cnt_elems;  /* int32 arrival counters needed (0 if no split) */
+    int32_t grid;       /* workgroups of the GEMM kernel = n_dp + n_split * split */
+    int32_t launches;   /* kernels enqueued: 1, or 2 with the split-K reduction */
     int64_t ws_elems;   /* fp32 workspace elements needed (0 if no split) */
     int32_t lds_bytes;  /* LDS used per workgroup */
+    int32_t threads;    /* threads per workgroup */
     int32_t kernel_id;  /* index of the compiled kernel instance */
 } fp8bg_plan;
 
-/* Library ABI version (bumped on any signature or struct change). */
+/* Library ABI version: FP8BG_ABI_VERSION of the build. */
 int fp8bg_version(void);
 
 /* Number of compute units of `device` (replaces _num_sms,
@@ -107,22 +131,23 @@ int fp8bg_num_cus(int device, int32_t* num_cus);
 int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg,
                     int32_t num_cus, fp8bg_plan* plan);
 
-/* 1 if this tile/wave/k_fixed combination is compiled into the library. */
+/* 1 if this kind/tile/wave/k_fixed combination is compiled into the library. */
 int fp8bg_config_supported(const fp8bg_config* cfg);
 
 /*
- * The GEMM.  Enqueues one kernel on `stream` (a hipStream_t; NULL = default
- * stream) and returns without synchronising.  Replaces the L0 host wrappers
+ * The GEMM.  Enqueues the kernel (plus the split-K reduction when the plan
+ * splits) on `stream` (a hipStream_t; NULL = default stream) and returns
+ * without synchronising.  Replaces the L0 host wrappers
  *   block_fp8_gemm_triton_h20  (kernels/baseline_triton.py:87-114)
  *   block_fp8_gemm_gluon_h20   (kernels/baseline_gluon.py:259-293)
  *   block_fp8_gemm_v2          (kernels/kernel_v2.py:339-376)
  *   block_fp8_gemm_scale_tma   (kernels/kernel_scale_tma.py:356-396)
  *   shortk                     (kernels/kernel_shortk.py:46-54)
- * with the caller owning C (bf16 [M,N], row stride N), the fp32 split-K
- * workspace `ws` (>= plan.ws_elems) and the int32 counters `cnt`
- * (>= plan.cnt_elems, zero before the first call; every call leaves them
- * zero again, so calls may be captured in a hipGraph and replayed).
- * Calls that share `ws`/`cnt` must be ordered (same stream).
+ * with the caller owning C (bf16 [M,N], row stride N) and the fp32 split-K
+ * workspace `ws` (>= plan.ws_elems elements, 16-byte aligned; unused and may
+ * be NULL when plan.n_split == 0).  Calls that share `ws` must be ordered
+ * (same stream); a captured hipGraph keeps using the `ws` it was captured
+ * with, so that buffer must outlive the graph.
  * Scale strides are in elements.  A, B and C must be 16-byte aligned.
  */
 int fp8bg_gemm(const void* A, const void* B,
@@ -130,7 +155,7 @@ int fp8bg_gemm(const void* A, const void* B,
                const float* Bs, int64_t bs_stride_n, int64_t bs_stride_k,
                void* C, int32_t M, int32_t N, int32_t K,
                const fp8bg_config* cfg, int32_t num_cus,
-               float* ws, int64_t ws_elems, int32_t* cnt, int32_t cnt_elems,
+               float* ws, int64_t ws_elems,
                void* stream);
 
 /* Static message for an error code. */
