@@ -24,6 +24,7 @@ ERR_NULL = 7
 
 KIND_TILED = 0
 KIND_SKINNY = 1
+KIND_RING = 2
 
 SPLIT_NONE = 0
 SPLIT_TAIL = 1
@@ -53,6 +54,7 @@ class Config(ctypes.Structure):
         ("waves_t", ctypes.c_int32),
         ("waves_k", ctypes.c_int32),
         ("unroll", ctypes.c_int32),
+        ("stages", ctypes.c_int32),
         ("split", ctypes.c_int32),
         ("split_mode", ctypes.c_int32),
         ("group_t", ctypes.c_int32),

@@ -32,6 +32,10 @@
 //                   tile among themselves (deep memory-level parallelism for
 //                   weight streaming); the S partial tiles are summed through
 //                   LDS in fixed wave order.
+//  * fp8bg_ring   - large-tile kernel: direct global->LDS loads
+//                   (global_load_lds_dwordx4) into an ST-stage LDS ring, one
+//                   barrier per 128-K group, 4 or 8 waves; same epilogue and
+//                   split-K handling as fp8bg_tiled.
 //  * fp8bg_split_reduce - fixed-order sum of split-K partials -> bf16.
 // Every reduction order is fixed by the configuration, so results are bitwise
 // reproducible run to run and under hipGraph replay.  No kernel uses atomics,
@@ -331,6 +335,188 @@ __global__ __launch_bounds__(kThreads) void fp8bg_tiled(KArgs a) {
 }
 
 // ===========================================================================
+// LDS-ring kernel: direct global->LDS loads, ST-stage ring, one barrier per group
+// ===========================================================================
+// s_waitcnt immediate (gfx9 encoding) that waits for vmcnt <= N only:
+// vmcnt in bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] at maximum.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+#define FP8BG_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// Workgroup tile TW weight rows x TT tokens, WW x WT waves.  Each 128-K group
+// of the stacked [weights; tokens] tile (TW + TT rows of 128 bytes) is copied
+// global -> LDS by global_load_lds_dwordx4: one instruction moves 64 lanes x
+// 16 bytes = 8 rows into a contiguous 1 KB block, lane l writing chunk slot
+// l % 8 of row l / 8.  The lane fetches global chunk (l % 8) ^ (row % 8), so
+// chunk c of a row sits at slot c ^ (row % 8): the XOR swizzle that keeps the
+// MFMA operand reads (8 consecutive lanes = 8 consecutive rows, same chunk)
+// on distinct banks.  ST stages form a ring: the loads of group i + ST - 1
+// are issued while group i is computed, with no register staging, and each
+// group needs one barrier.
+template <int TW, int TT, int WW, int WT, int ST, int KF>
+__global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
+    constexpr int NWAVE = WW * WT;
+    constexpr int WTW = TW / WW;
+    constexpr int WTT = TT / WT;
+    constexpr int NW = WTW / 16;
+    constexpr int NT = WTT / 16;
+    constexpr int ROWS = TW + TT;
+    constexpr int NJ = ROWS / (8 * NWAVE);        // 1 KB DMA blocks per wave per group
+    constexpr int STAGE = ROWS * kRowBytes;
+    static_assert(WTW % 16 == 0 && WTT % 16 == 0 && NW >= 1 && NT >= 1, "wave tile");
+    static_assert(ROWS % (8 * NWAVE) == 0 && NJ >= 1, "DMA blocks per wave");
+    static_assert(ST >= 2, "ring depth");
+    static_assert(ST * STAGE <= kMaxLds, "LDS");
+
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[ST * STAGE];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wv_w = wave % WW, wv_t = wave / WW;
+
+    // ---- tile decode ----
+    const int KG = KF ? KF : (a.K / kGroupK);
+    int pid = blockIdx.x;
+    int tile, sidx = 0, kcount, k_lo;
+    if (pid < a.n_dp) {
+        if (a.xcd_remap) pid = xcd_remap(pid, a.n_dp);
+        tile = pid;
+        k_lo = 0;
+        kcount = KG;
+    } else {
+        const int q = pid - a.n_dp;
+        tile = a.n_dp + q / a.split;
+        sidx = q % a.split;
+        kcount = KG / a.split;
+        k_lo = sidx * kcount;
+    }
+    int w0, t0;
+    tile_origin(tile, a, w0, t0);
+
+    // ---- DMA sources: block b = wave * NJ + j holds rows 8b .. 8b+7 ----
+    const uint8_t* sbase[NJ];
+    uint32_t soff[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int b = wave * NJ + j;
+        const int row = 8 * b + (lane >> 3);
+        const int chunk = (lane & 7) ^ (row & 7);
+        if (8 * b < TW) {
+            sbase[j] = a.B;
+            soff[j] = (uint32_t)min(w0 + row, a.N - 1) * (uint32_t)a.K + chunk * 16;
+        } else {
+            sbase[j] = a.A;
+            soff[j] = (uint32_t)min(t0 + row - TW, a.M - 1) * (uint32_t)a.K + chunk * 16;
+        }
+    }
+    auto dma = [&](int g, int stage) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(sbase[j] + soff[j] + (uint32_t)g * kGroupK),
+                FP8BG_LDS_PTR(lds + stage * STAGE + (wave * NJ + j) * 1024), 16, 0, 0);
+    };
+
+    // ---- scales ----
+    const float* asp[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+        asp[t] = a.As + (int64_t)min(t0 + wv_t * WTT + t * 16 + (lane & 15), a.M - 1) * a.as_sm;
+    const float* bsp[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+        bsp[w] = a.Bs + (int64_t)min((w0 + wv_w * WTW + w * 16) >> 7, a.N / 128 - 1) * a.bs_sn;
+    float sa_n[NT], sb_n[NW];
+    auto sload = [&](int g) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) sa_n[t] = asp[t][(int64_t)g * a.as_sk];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sb_n[w] = bsp[w][(int64_t)g * a.bs_sk];
+    };
+
+    f32x4 acc[NW][NT];
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[w][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    const int c0 = ((lane >> 4) * 2) ^ (lane & 7);
+    auto opread = [&](const unsigned char* st, int row) -> i32x8 {
+        const unsigned char* base = st + row * kRowBytes;
+        const i32x4 lo = *(const i32x4*)(base + (c0 << 4));
+        const i32x4 hi = *(const i32x4*)(base + ((c0 ^ 1) << 4));
+        return (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+
+#pragma unroll
+    for (int s = 0; s < ST - 1; ++s)
+        if (s < kcount) dma(k_lo + s, s);
+    sload(k_lo);
+
+#pragma unroll (KF ? KF : 1)
+    for (int i = 0; i < kcount; ++i) {
+        // Stage i is complete once at most the DMA blocks of the ST - 2
+        // later groups are outstanding (vmcnt retires in issue order; any
+        // scale loads issued after it only make the wait stricter).
+        if (i + ST - 2 < kcount)
+            wait_vmcnt<NJ * (ST - 2)>();
+        else
+            wait_vmcnt<0>();
+        // All waves' blocks of stage i have landed, and every wave has
+        // finished reading stage (i - 1) % ST, which is refilled next.
+        __builtin_amdgcn_s_barrier();
+        if (i + ST - 1 < kcount) dma(k_lo + i + ST - 1, (i + ST - 1) % ST);
+        float sa[NT], sb[NW];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) sa[t] = sa_n[t];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sb[w] = sb_n[w];
+        if (i + 1 < kcount) sload(k_lo + i + 1);
+
+        const unsigned char* st = lds + (i % ST) * STAGE;
+        i32x8 wop[NW];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) wop[w] = opread(st, wv_w * WTW + w * 16 + (lane & 15));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const i32x8 top = opread(st, TW + wv_t * WTT + t * 16 + (lane & 15));
+#pragma unroll
+            for (int w = 0; w < NW; ++w) promote(acc[w][t], mfma16x16x128(wop[w], top), sa[t] * sb[w]);
+        }
+    }
+
+    // ---- epilogue (as fp8bg_tiled) ----
+    if (blockIdx.x < a.n_dp) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int m = t0 + wv_t * WTT + t * 16 + (lane & 15);
+            if (m >= a.M) continue;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const int n = w0 + wv_w * WTW + w * 16 + (lane >> 4) * 4;
+                if (n >= a.N) continue;
+                *(uint2*)(a.C + (size_t)m * a.N + n) = pack_bf16x4(acc[w][t]);
+            }
+        }
+        return;
+    }
+    float* mine = a.ws + ((size_t)(tile - a.n_dp) * a.split + sidx) * (size_t)(TW * TT);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int tl = wv_t * WTT + t * 16 + (lane & 15);
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const int wl = wv_w * WTW + w * 16 + (lane >> 4) * 4;
+            *(f32x4*)(mine + tl * TW + wl) = acc[w][t];
+        }
+    }
+}
+
+// ===========================================================================
 // Small-M kernel: operands straight from global memory, waves split K
 // ===========================================================================
 template <int NWB, int NTB, int S, int U>
@@ -501,8 +687,17 @@ __global__ __launch_bounds__(kThreads) void fp8bg_split_reduce(KArgs a, int skin
     X(2, 4, 4, 2) X(2, 4, 8, 1) X(2, 4, 8, 2)                                  \
     X(4, 4, 4, 1) X(4, 4, 8, 1) X(4, 4, 4, 2)
 
+// ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed)
+#define FP8BG_RING(X)                                                          \
+    X(256, 128, 4, 1, 3, 0) X(256, 128, 2, 2, 3, 0) X(128, 256, 2, 2, 3, 0)    \
+    X(128, 128, 2, 2, 4, 0) X(128, 128, 4, 1, 4, 0) X(128, 128, 2, 2, 3, 0)    \
+    X(128, 64, 2, 2, 4, 0) X(128, 64, 4, 1, 4, 0) X(128, 64, 2, 2, 3, 0)       \
+    X(64, 64, 4, 1, 4, 0) X(256, 64, 4, 1, 3, 0) X(128, 32, 4, 1, 4, 0)        \
+    X(256, 256, 4, 2, 2, 0) X(256, 256, 2, 4, 2, 0) X(256, 128, 4, 2, 3, 0)    \
+    X(512, 128, 8, 1, 2, 0) X(256, 128, 4, 1, 2, 2) X(128, 128, 2, 2, 2, 2)
+
 struct Instance {
-    int kind, tw, tt, ww, wt, wk, unroll, kf, threads;
+    int kind, tw, tt, ww, wt, wk, unroll, stages, kf, threads;
     void (*launch)(dim3 grid, size_t shm, hipStream_t s, const KArgs& a);
 };
 
@@ -522,13 +717,27 @@ FP8BG_TILED(FP8BG_TILED_LAUNCHER)
 FP8BG_SKINNY(FP8BG_SKINNY_LAUNCHER)
 #undef FP8BG_SKINNY_LAUNCHER
 
+#define FP8BG_RING_LAUNCHER(TW, TT, WW, WT, ST, KF)                                          \
+    static void ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF(dim3 g, size_t shm,            \
+                                                             hipStream_t s, const KArgs& a) { \
+        hipLaunchKernelGGL((fp8bg_ring<TW, TT, WW, WT, ST, KF>), g, dim3(64 * WW * WT), shm, \
+                           s, a);                                                             \
+    }
+FP8BG_RING(FP8BG_RING_LAUNCHER)
+#undef FP8BG_RING_LAUNCHER
+
 #define FP8BG_TILED_ENTRY(TW, TT, WW, WT, KF) \
-    {FP8BG_KIND_TILED, TW, TT, WW, WT, 1, 1, KF, kThreads, tiled_##TW##_##TT##_##WW##_##WT##_##KF},
+    {FP8BG_KIND_TILED, TW, TT, WW, WT, 1, 1, 1, KF, kThreads, tiled_##TW##_##TT##_##WW##_##WT##_##KF},
 #define FP8BG_SKINNY_ENTRY(NW, NT, S, U) \
-    {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 0, 64 * S, skinny_##NW##_##NT##_##S##_##U},
-const Instance kInstances[] = {FP8BG_TILED(FP8BG_TILED_ENTRY) FP8BG_SKINNY(FP8BG_SKINNY_ENTRY)};
+    {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 1, 0, 64 * S, skinny_##NW##_##NT##_##S##_##U},
+#define FP8BG_RING_ENTRY(TW, TT, WW, WT, ST, KF)                                  \
+    {FP8BG_KIND_RING, TW, TT, WW, WT, 1, 1, ST, KF, 64 * WW * WT,                 \
+     ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF},
+const Instance kInstances[] = {FP8BG_TILED(FP8BG_TILED_ENTRY) FP8BG_SKINNY(FP8BG_SKINNY_ENTRY)
+                                   FP8BG_RING(FP8BG_RING_ENTRY)};
 #undef FP8BG_TILED_ENTRY
 #undef FP8BG_SKINNY_ENTRY
+#undef FP8BG_RING_ENTRY
 constexpr int kNumInstances = sizeof(kInstances) / sizeof(kInstances[0]);
 
 int find_instance(const fp8bg_config* c) {
@@ -540,6 +749,9 @@ int find_instance(const fp8bg_config* c) {
             return i;
         if (k.kind == FP8BG_KIND_SKINNY && k.wk == c->waves_k && k.unroll == c->unroll &&
             c->k_fixed == 0)
+            return i;
+        if (k.kind == FP8BG_KIND_RING && k.ww == c->waves_w && k.wt == c->waves_t &&
+            k.stages == c->stages && k.kf == c->k_fixed)
             return i;
     }
     return -1;
@@ -591,7 +803,10 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     const Instance& k = kInstances[ki];
     if (k.kf && kg != k.kf) return FP8BG_ERR_CONFIG;
     const bool skinny = k.kind == FP8BG_KIND_SKINNY;
-    if (skinny && (cfg->flags & FP8BG_FLAG_SCALE_LDS)) return FP8BG_ERR_CONFIG;
+    const bool ring = k.kind == FP8BG_KIND_RING;
+    if ((skinny || ring) && (cfg->flags & FP8BG_FLAG_SCALE_LDS)) return FP8BG_ERR_CONFIG;
+    // the ring kernel addresses A and B with 32-bit byte offsets
+    if (ring && ((int64_t)M * K > 0xffffffffLL || (int64_t)N * K > 0xffffffffLL)) return FP8BG_ERR_SHAPE;
 
     int split = (cfg->split_mode == FP8BG_SPLIT_NONE || k.kf) ? 1 : cfg->split;
     if (kg % split) split = 1;  // reference baseline_gluon.py:274-276
@@ -608,6 +823,8 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     int64_t lds;
     if (skinny) {
         lds = (int64_t)k.wk * (k.tw / 16) * (k.tt / 16) * 64 * 16;
+    } else if (ring) {
+        lds = (int64_t)k.stages * (k.tw + k.tt) * 128;
     } else {
         lds = 2LL * (k.tw + k.tt) * 128;
         if (cfg->flags & FP8BG_FLAG_SCALE_LDS) lds += (int64_t)k.tt * kg * 4;

@@ -53,6 +53,11 @@ extern "C" {
  * summed in fixed wave order.  The reference's SWAP_AB small-M role
  * (kernels/baseline_gluon.py:77-83). */
 #define FP8BG_KIND_SKINNY 1
+/* LDS-ring kernel: like FP8BG_KIND_TILED, but each 128-K group is copied
+ * global -> LDS by direct-to-LDS loads into a `stages`-deep ring (no register
+ * staging, one barrier per group); 4 or 8 waves.  Requires M*K and N*K below
+ * 2^32. */
+#define FP8BG_KIND_RING   2
 
 /* ---- split-K modes ------------------------------------------------------ */
 /* No split: every tile runs the full K range (config split ignored). */
@@ -84,10 +89,11 @@ typedef struct fp8bg_config {
     int32_t kind;       /* FP8BG_KIND_* */
     int32_t block_w;    /* weight rows (N) per workgroup tile */
     int32_t block_t;    /* tokens (M) per workgroup tile */
-    int32_t waves_w;    /* tiled: waves along N inside the tile (waves_w*waves_t == 4) */
-    int32_t waves_t;    /* tiled: waves along M inside the tile */
+    int32_t waves_w;    /* tiled/ring: waves along N inside the tile */
+    int32_t waves_t;    /* tiled/ring: waves along M inside the tile */
     int32_t waves_k;    /* skinny: waves splitting K inside a workgroup (4 or 8) */
     int32_t unroll;     /* skinny: 128-K groups in flight per wave */
+    int32_t stages;     /* ring: LDS ring depth in 128-K groups */
     int32_t split;      /* cross-workgroup K split factor, in 128-K groups;
                            normalised to 1 when it does not divide K/128
                            (baseline_gluon.py:274-276) */
@@ -95,8 +101,9 @@ typedef struct fp8bg_config {
     int32_t group_t;    /* tiled: token-tile swizzle group (GROUP_SIZE_M
                            semantics, baseline_triton.py:36-45); >= 1 */
     int32_t flags;      /* FP8BG_FLAG_* */
-    int32_t k_fixed;    /* tiled: 0 = runtime K loop; 2 = K==256 short-K kernel
-                           with no K loop (reference kernels/kernel_shortk.py:11-54) */
+    int32_t k_fixed;    /* tiled/ring: 0 = runtime K loop; 2 = K==256 short-K
+                           kernel with no K loop (reference
+                           kernels/kernel_shortk.py:11-54) */
 } fp8bg_config;
 
 /*
