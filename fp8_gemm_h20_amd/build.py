@@ -1,7 +1,8 @@
 """Build libfp8bg.so in-tree: `python -m fp8_gemm_h20_amd.build`.
 
 hipcc cross-compiles for gfx950 without a GPU.  Packed-fp32 VALU forms are
-disabled for all device code (-packed-fp32-ops).
+disabled for all device code (-packed-fp32-ops), and MFMA instructions use the
+VGPR form for their results (-amdgpu-mfma-vgpr-form).
 """
 import os
 import shutil
@@ -27,6 +28,9 @@ def hipcc():
 def command(out=OUT):
     return [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-shared", "-fPIC",
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            # MFMA results in VGPRs: every partial product is promoted by VALU
+            # FMAs right away, so AGPR destinations only add copies
+            "-mllvm", "-amdgpu-mfma-vgpr-form=1",
             f"-I{INCLUDE}", "-o", str(out), str(SRC)]
 
 

@@ -53,8 +53,12 @@ def weight_tile(entry):
 
 def _native_ok(impl, c, k):
     """A gfx950-native entry names a compiled kernel instance."""
-    from .kernels import TILED, SKINNY_TILES
+    from .kernels import TILED, SKINNY_TILES, RING
     tw, tt = c.get("BLOCK_W"), c.get("BLOCK_T")
+    if impl == "ring":
+        kf = c.get("K_FIXED", 0)
+        return (c.get("SPLIT_MODE", "none") in _SPLIT_MODES and (kf == 0 or k == 256 * kf // 2) and
+                (tw, tt, c.get("WAVES_W"), c.get("WAVES_T"), c.get("STAGES"), kf) in RING)
     if impl == "skinny":
         mode = c.get("SPLIT_MODE", "none")
         return (mode in ("none", "full") and

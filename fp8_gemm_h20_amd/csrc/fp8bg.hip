@@ -345,6 +345,13 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Same, and also wait for every LDS read of this wave (lgkmcnt = 0).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lds() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
 #define FP8BG_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
 // Workgroup tile TW weight rows x TT tokens, WW x WT waves.  Each 128-K group
@@ -354,9 +361,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 // l % 8 of row l / 8.  The lane fetches global chunk (l % 8) ^ (row % 8), so
 // chunk c of a row sits at slot c ^ (row % 8): the XOR swizzle that keeps the
 // MFMA operand reads (8 consecutive lanes = 8 consecutive rows, same chunk)
-// on distinct banks.  ST stages form a ring: the loads of group i + ST - 1
-// are issued while group i is computed, with no register staging, and each
-// group needs one barrier.
+// on distinct banks.  The group's scales travel the same way: one
+// global_load_lds_dword per wave fills a 64-float slice of the stage's scale
+// area with the tile's As column (slots 0 .. TT-1) and its Bs values (slots
+// TT .. TT + TW/128 - 1).  ST stages form a ring: the loads of group
+// i + ST - 1 are issued while group i is computed, with no register staging
+// and no VGPR-destination memory loads in the loop, and each group needs one
+// barrier.
 template <int TW, int TT, int WW, int WT, int ST, int KF>
 __global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
     constexpr int NWAVE = WW * WT;
@@ -365,11 +376,17 @@ __global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
     constexpr int NW = WTW / 16;
     constexpr int NT = WTT / 16;
     constexpr int ROWS = TW + TT;
-    constexpr int NJ = ROWS / (8 * NWAVE);        // 1 KB DMA blocks per wave per group
-    constexpr int STAGE = ROWS * kRowBytes;
+    constexpr int NJ = ROWS / (8 * NWAVE);        // 1 KB operand blocks per wave per group
+    constexpr int NDMA = NJ + 1;                  // + one scale slice per wave
+    constexpr int OPS = ROWS * kRowBytes;         // operand bytes per stage
+    constexpr int SCALES = NWAVE * 64;            // scale slots per stage
+    constexpr int STAGE = OPS + SCALES * 4;
     static_assert(WTW % 16 == 0 && WTT % 16 == 0 && NW >= 1 && NT >= 1, "wave tile");
     static_assert(ROWS % (8 * NWAVE) == 0 && NJ >= 1, "DMA blocks per wave");
-    static_assert(ST >= 2, "ring depth");
+    constexpr int NBS = (TW + 127) / 128;         // Bs blocks the tile spans
+    static_assert(TT + NBS <= SCALES, "scale slots");
+    static_assert(WTW <= 128 && 128 % WTW == 0, "wave weight rows inside one Bs block");
+    static_assert(ST >= 2 && NDMA * (ST - 2) < 64, "ring depth");
     static_assert(ST * STAGE <= kMaxLds, "LDS");
 
     __shared__ __attribute__((aligned(1024))) unsigned char lds[ST * STAGE];
@@ -397,7 +414,7 @@ __global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
     int w0, t0;
     tile_origin(tile, a, w0, t0);
 
-    // ---- DMA sources: block b = wave * NJ + j holds rows 8b .. 8b+7 ----
+    // ---- DMA sources: operand block b = wave * NJ + j holds rows 8b .. 8b+7 ----
     const uint8_t* sbase[NJ];
     uint32_t soff[NJ];
 #pragma unroll
@@ -413,29 +430,31 @@ __global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
             soff[j] = (uint32_t)min(t0 + row - TW, a.M - 1) * (uint32_t)a.K + chunk * 16;
         }
     }
+    // scale slot q = 64 * wave + lane: As of token t0 + q, then Bs of weight
+    // block w0 / 128 + (q - TT) for the NBS blocks the tile spans; spare
+    // slots reload As[0, g] (never read)
+    const int q = 64 * wave + lane;
+    const float* sc_base;
+    int64_t sc_step;
+    if (q < TT) {
+        sc_base = a.As + (int64_t)min(t0 + q, a.M - 1) * a.as_sm;
+        sc_step = a.as_sk;
+    } else if (q < TT + NBS) {
+        sc_base = a.Bs + (int64_t)min(w0 / 128 + (q - TT), a.N / 128 - 1) * a.bs_sn;
+        sc_step = a.bs_sk;
+    } else {
+        sc_base = a.As;
+        sc_step = a.as_sk;
+    }
     auto dma = [&](int g, int stage) {
+        unsigned char* st = lds + stage * STAGE;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
             __builtin_amdgcn_global_load_lds(
-                (const void*)(sbase[j] + soff[j] + (uint32_t)g * kGroupK),
-                FP8BG_LDS_PTR(lds + stage * STAGE + (wave * NJ + j) * 1024), 16, 0, 0);
-    };
-
-    // ---- scales ----
-    const float* asp[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-        asp[t] = a.As + (int64_t)min(t0 + wv_t * WTT + t * 16 + (lane & 15), a.M - 1) * a.as_sm;
-    const float* bsp[NW];
-#pragma unroll
-    for (int w = 0; w < NW; ++w)
-        bsp[w] = a.Bs + (int64_t)min((w0 + wv_w * WTW + w * 16) >> 7, a.N / 128 - 1) * a.bs_sn;
-    float sa_n[NT], sb_n[NW];
-    auto sload = [&](int g) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) sa_n[t] = asp[t][(int64_t)g * a.as_sk];
-#pragma unroll
-        for (int w = 0; w < NW; ++w) sb_n[w] = bsp[w][(int64_t)g * a.bs_sk];
+                (const void*)(sbase[j] + (uint32_t)(soff[j] + (uint32_t)g * kGroupK)),
+                FP8BG_LDS_PTR(st + (wave * NJ + j) * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(sc_base + (int64_t)g * sc_step),
+                                         FP8BG_LDS_PTR(st + OPS + wave * 256), 4, 0, 0);
     };
 
     f32x4 acc[NW][NT];
@@ -452,42 +471,47 @@ __global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
         return (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
 
+    // Every step issues its loads unconditionally so the vmcnt bookkeeping is
+    // the same in every iteration: group indices past the range are clamped
+    // to the last group (an L2 hit), and such a load lands in a stage that no
+    // later step reads (stage (i + ST - 1) % ST with i + ST - 1 >= kcount is
+    // only read again at step i + ST - 1).
+    const int g_last = k_lo + kcount - 1;
 #pragma unroll
-    for (int s = 0; s < ST - 1; ++s)
-        if (s < kcount) dma(k_lo + s, s);
-    sload(k_lo);
+    for (int s = 0; s < ST - 1; ++s) dma(min(k_lo + s, g_last), s);
 
 #pragma unroll (KF ? KF : 1)
     for (int i = 0; i < kcount; ++i) {
-        // Stage i is complete once at most the DMA blocks of the ST - 2
-        // later groups are outstanding (vmcnt retires in issue order; any
-        // scale loads issued after it only make the wait stricter).
-        if (i + ST - 2 < kcount)
-            wait_vmcnt<NJ * (ST - 2)>();
-        else
-            wait_vmcnt<0>();
-        // All waves' blocks of stage i have landed, and every wave has
-        // finished reading stage (i - 1) % ST, which is refilled next.
+        // Stage i is complete once at most the DMA instructions of the ST - 2
+        // later steps are outstanding (vmcnt retires in issue order); this
+        // wave's LDS reads of stage (i - 1) % ST have all returned.
+        wait_vmcnt_lds<NDMA * (ST - 2)>();
+        // All waves' blocks of stage i have landed, and every wave is done
+        // reading stage (i - 1) % ST, which is refilled next.  The empty asm
+        // statements keep the compiler from moving LDS reads or writes
+        // across the barrier.
+        asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
-        if (i + ST - 1 < kcount) dma(k_lo + i + ST - 1, (i + ST - 1) % ST);
-        float sa[NT], sb[NW];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) sa[t] = sa_n[t];
-#pragma unroll
-        for (int w = 0; w < NW; ++w) sb[w] = sb_n[w];
-        if (i + 1 < kcount) sload(k_lo + i + 1);
+        asm volatile("" ::: "memory");
+        dma(min(k_lo + i + ST - 1, g_last), (i + ST - 1) % ST);
 
         const unsigned char* st = lds + (i % ST) * STAGE;
+        const float* sc = (const float*)(st + OPS);
+        const float sb = sc[TT + (w0 % 128 + wv_w * WTW) / 128];
         i32x8 wop[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) wop[w] = opread(st, wv_w * WTW + w * 16 + (lane & 15));
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
+            const float s_t = sc[wv_t * WTT + t * 16 + (lane & 15)] * sb;
             const i32x8 top = opread(st, TW + wv_t * WTT + t * 16 + (lane & 15));
 #pragma unroll
-            for (int w = 0; w < NW; ++w) promote(acc[w][t], mfma16x16x128(wop[w], top), sa[t] * sb[w]);
+            for (int w = 0; w < NW; ++w) promote(acc[w][t], mfma16x16x128(wop[w], top), s_t);
         }
     }
+    // The clamped loads of the last ST - 1 steps are still in flight: they
+    // must land before the workgroup's LDS can be handed to another one.
+    wait_vmcnt<0>();
 
     // ---- epilogue (as fp8bg_tiled) ----
     if (blockIdx.x < a.n_dp) {
@@ -689,12 +713,12 @@ __global__ __launch_bounds__(kThreads) void fp8bg_split_reduce(KArgs a, int skin
 
 // ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed)
 #define FP8BG_RING(X)                                                          \
-    X(256, 128, 4, 1, 3, 0) X(256, 128, 2, 2, 3, 0) X(128, 256, 2, 2, 3, 0)    \
-    X(128, 128, 2, 2, 4, 0) X(128, 128, 4, 1, 4, 0) X(128, 128, 2, 2, 3, 0)    \
-    X(128, 64, 2, 2, 4, 0) X(128, 64, 4, 1, 4, 0) X(128, 64, 2, 2, 3, 0)       \
-    X(64, 64, 4, 1, 4, 0) X(256, 64, 4, 1, 3, 0) X(128, 32, 4, 1, 4, 0)        \
-    X(256, 256, 4, 2, 2, 0) X(256, 256, 2, 4, 2, 0) X(256, 128, 4, 2, 3, 0)    \
-    X(512, 128, 8, 1, 2, 0) X(256, 128, 4, 1, 2, 2) X(128, 128, 2, 2, 2, 2)
+    X(256, 128, 4, 1, 3, 0) X(256, 128, 2, 2, 3, 0) X(128, 128, 2, 2, 4, 0)    \
+    X(128, 128, 4, 1, 4, 0) X(128, 128, 2, 2, 3, 0) X(128, 64, 2, 2, 4, 0)     \
+    X(128, 64, 4, 1, 4, 0) X(128, 64, 2, 2, 3, 0) X(64, 64, 4, 1, 4, 0)        \
+    X(256, 64, 4, 1, 3, 0) X(128, 32, 4, 1, 4, 0) X(256, 256, 4, 2, 2, 0)      \
+    X(256, 128, 4, 2, 3, 0) X(256, 128, 4, 2, 2, 0) X(128, 256, 2, 4, 2, 0)    \
+    X(256, 128, 4, 1, 2, 2) X(128, 128, 2, 2, 2, 2)
 
 struct Instance {
     int kind, tw, tt, ww, wt, wk, unroll, stages, kf, threads;
@@ -824,7 +848,7 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     if (skinny) {
         lds = (int64_t)k.wk * (k.tw / 16) * (k.tt / 16) * 64 * 16;
     } else if (ring) {
-        lds = (int64_t)k.stages * (k.tw + k.tt) * 128;
+        lds = (int64_t)k.stages * ((k.tw + k.tt) * 128 + k.ww * k.wt * 64 * 4);
     } else {
         lds = 2LL * (k.tw + k.tt) * 128;
         if (cfg->flags & FP8BG_FLAG_SCALE_LDS) lds += (int64_t)k.tt * kg * 4;

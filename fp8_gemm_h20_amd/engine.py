@@ -7,6 +7,7 @@ touches the GPU.  `run(entry, args)` calls fn(A, B, As, Bs, dict(config)).
 gfx950-native impls written by this package's tables:
   tiled   LDS-tiled MFMA kernel, optional tail or full split-K
   skinny  small-M kernel: operands straight to registers, waves split K
+  ring    large-tile kernel: direct-to-LDS ring, one barrier per K group
   shortk  K == 256 kernel, no K loop (also accepts the reference's BM/BN keys)
 Reference H20 impl names, accepted so reference tables keep working; each
 runs on the gfx950 kernels (see kernels.py):
@@ -18,6 +19,7 @@ from importlib import import_module
 KERNELS = {
     "tiled": ("kernels", "tiled"),
     "skinny": ("kernels", "skinny"),
+    "ring": ("kernels", "ring"),
     "shortk": ("kernels", "shortk"),
     "triton": ("kernels", "triton"),
     "gluon": ("kernels", "gluon"),
@@ -26,7 +28,7 @@ KERNELS = {
 }
 
 # impls whose config uses this package's gfx950 keys
-NATIVE = ("tiled", "skinny", "shortk")
+NATIVE = ("tiled", "skinny", "ring", "shortk")
 
 
 @lru_cache(maxsize=None)

@@ -14,6 +14,8 @@ Two families of config dicts are accepted:
     GROUP_SIZE_M, SCALE_LDS, XCD_REMAP (LDS-tiled kernel);
   - impl "skinny": BLOCK_W, BLOCK_T, WAVES_K, UNROLL, SPLIT, SPLIT_MODE,
     XCD_REMAP (small-M kernel, waves split K);
+  - impl "ring": BLOCK_W, BLOCK_T, WAVES_W, WAVES_T, STAGES, SPLIT,
+    SPLIT_MODE, GROUP_SIZE_M, XCD_REMAP (direct-to-LDS ring kernel);
   - impl "shortk": BLOCK_W, BLOCK_T (K == 256, no K loop).
 * the reference's H20 entries (impl "triton", "gluon", "v2", "scale_tma",
   "shortk" with BM/BN keys), translated onto the nearest compiled gfx950 tile
@@ -51,6 +53,15 @@ SKINNY = (
 )
 # skinny instances as (block_w, block_t, waves_k, unroll)
 SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
+# ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed)
+RING = (
+    (256, 128, 4, 1, 3, 0), (256, 128, 2, 2, 3, 0), (128, 128, 2, 2, 4, 0),
+    (128, 128, 4, 1, 4, 0), (128, 128, 2, 2, 3, 0), (128, 64, 2, 2, 4, 0),
+    (128, 64, 4, 1, 4, 0), (128, 64, 2, 2, 3, 0), (64, 64, 4, 1, 4, 0),
+    (256, 64, 4, 1, 3, 0), (128, 32, 4, 1, 4, 0), (256, 256, 4, 2, 2, 0),
+    (256, 128, 4, 2, 3, 0), (256, 128, 4, 2, 2, 0), (128, 256, 2, 4, 2, 0),
+    (256, 128, 4, 1, 2, 2), (128, 128, 2, 2, 2, 2),
+)
 # back-compat name used by tests and the tuner
 INSTANCES = TILED
 
@@ -113,15 +124,23 @@ def tiled_struct(cfg, k_fixed=0):
         if waves is None:
             raise ValueError(f"no compiled gfx950 kernel for tile {tw}x{tt} (k_fixed={k_fixed})")
         ww, wt = waves
-    return _lib.Config(_lib.KIND_TILED, tw, tt, int(ww), int(wt), 1, 1, int(cfg.get("SPLIT", 1)),
+    return _lib.Config(_lib.KIND_TILED, tw, tt, int(ww), int(wt), 1, 1, 1, int(cfg.get("SPLIT", 1)),
                        _split_mode(cfg, "full"), int(cfg.get("GROUP_SIZE_M", 1)), _flags(cfg), k_fixed)
 
 
 def skinny_struct(cfg):
     """C config struct for a skinny config dict."""
     return _lib.Config(_lib.KIND_SKINNY, int(cfg["BLOCK_W"]), int(cfg["BLOCK_T"]), 1, 1,
-                       int(cfg.get("WAVES_K", 8)), int(cfg.get("UNROLL", 1)),
+                       int(cfg.get("WAVES_K", 8)), int(cfg.get("UNROLL", 1)), 1,
                        int(cfg.get("SPLIT", 1)), _split_mode(cfg, "none"), 1, _flags(cfg), 0)
+
+
+def ring_struct(cfg, k_fixed=0):
+    """C config struct for a ring config dict."""
+    return _lib.Config(_lib.KIND_RING, int(cfg["BLOCK_W"]), int(cfg["BLOCK_T"]),
+                       int(cfg["WAVES_W"]), int(cfg["WAVES_T"]), 1, 1, int(cfg["STAGES"]),
+                       int(cfg.get("SPLIT", 1)), _split_mode(cfg, "none"),
+                       int(cfg.get("GROUP_SIZE_M", 1)), _flags(cfg), k_fixed)
 
 
 # back-compat alias
@@ -229,6 +248,11 @@ def _skinny_cached(items):
     return skinny_struct(dict(items))
 
 
+@lru_cache(maxsize=1024)
+def _ring_cached(items, k_fixed):
+    return ring_struct(dict(items), k_fixed)
+
+
 # ---------------------------------------------------------------------------
 # gfx950-native impls
 # ---------------------------------------------------------------------------
@@ -240,6 +264,12 @@ def tiled(A, B, As, Bs, config):
 def skinny(A, B, As, Bs, config):
     """Small-M kernel: operands straight to registers, waves split K."""
     return launch(A, B, As, Bs, _skinny_cached(_freeze(config)))
+
+
+def ring(A, B, As, Bs, config):
+    """Large-tile kernel: direct-to-LDS ring, one barrier per K group.
+    K_FIXED=2 selects the K == 256 instance with both groups unrolled."""
+    return launch(A, B, As, Bs, _ring_cached(_freeze(config), int(config.get("K_FIXED", 0))))
 
 
 def shortk(A, B, As, Bs, config):
