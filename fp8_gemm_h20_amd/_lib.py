@@ -32,6 +32,8 @@ SPLIT_FULL = 2
 
 FLAG_SCALE_LDS = 0x1
 FLAG_XCD_REMAP = 0x2
+FLAG_SWZ8 = 0x4
+FLAG_SWZPAIR = 0x8
 
 # Every symbol include/fp8bg.h declares.
 EXPORTS = (

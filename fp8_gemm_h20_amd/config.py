@@ -55,6 +55,8 @@ def _native_ok(impl, c, k):
     """A gfx950-native entry names a compiled kernel instance."""
     from .kernels import TILED, SKINNY_TILES, RING
     tw, tt = c.get("BLOCK_W"), c.get("BLOCK_T")
+    if c.get("LDS_SWIZZLE", "row16") not in ("row8", "row16", "pair"):
+        return False
     if impl == "ring":
         kf = c.get("K_FIXED", 0)
         return (c.get("SPLIT_MODE", "none") in _SPLIT_MODES and (kf == 0 or k == 256 * kf // 2) and

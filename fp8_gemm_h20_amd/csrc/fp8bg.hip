@@ -73,6 +73,7 @@ struct KArgs {
     int group_t;           // token-tile swizzle group
     int xcd_remap;
     int scale_lds;
+    int swz;               // LDS swizzle mode (see swz())
 };
 
 // fp32 -> bf16 bits, round to nearest even; any NaN -> 0x7fc0 (as torch).
@@ -117,6 +118,19 @@ __device__ __forceinline__ int xcd_remap(int pid, int n) {
     const int per = n / kNumXcd, rem = n % kNumXcd;
     const int xcd = pid % kNumXcd, local = pid / kNumXcd;
     return xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
+// LDS row swizzle: 16-byte chunk c of tile row r is stored at chunk slot
+// c ^ swz(r).  Operand reads have lanes l .. l+15 read rows r0 .. r0+15 (r0 a
+// multiple of 16) at one logical chunk; the slot pattern decides how those 16
+// addresses spread over the LDS banks.
+//   mode 0: swz = (r & 7) ^ ((r >> 3) & 1)  (16-row pattern: any 16 consecutive
+//           rows read at one chunk hit distinct bank groups; measured free of
+//           LDS bank conflicts on gfx950 by SQ_LDS_BANK_CONFLICT)
+//   mode 1: swz = r & 7                    (8-row period)
+//   mode 2: swz = (r >> 1) & 7              (pairs of rows share a slot)
+__device__ __forceinline__ int swz(int r, int mode) {
+    return mode == 1 ? (r & 7) : mode == 2 ? ((r >> 1) & 7) : ((r & 7) ^ ((r >> 3) & 1));
 }
 
 // Grouped tile order (GROUP_SIZE_M semantics, reference
@@ -180,8 +194,9 @@ __global__ __launch_bounds__(kThreads) void fp8bg_tiled(KArgs a) {
 
     // ---- per-thread global->LDS chunk assignment (fixed across groups) ----
     // chunk c: row c/8 of the stacked [weights; tokens] tile, 16-byte column
-    // c%8, stored at column (c%8) ^ (row & 7) so that the operand reads (8
-    // consecutive lanes = 8 consecutive rows, same chunk) hit distinct banks.
+    // c%8, stored at slot (c%8) ^ swz(row) so that the operand reads (16
+    // consecutive lanes = 16 consecutive rows, same chunk) spread over the
+    // LDS banks.
     const uint8_t* gptr[NLD];
     int loff[NLD];
 #pragma unroll
@@ -196,7 +211,7 @@ __global__ __launch_bounds__(kThreads) void fp8bg_tiled(KArgs a) {
             const int m = min(t0 + row - TW, a.M - 1);
             gptr[j] = a.A + (size_t)m * a.K + col * 16;
         }
-        loff[j] = row * kRowBytes + ((col ^ (row & 7)) << 4);
+        loff[j] = row * kRowBytes + ((col ^ swz(row, a.swz)) << 4);
     }
     auto gload = [&](int g, i32x4 (&r)[NLD]) {
 #pragma unroll
@@ -261,7 +276,8 @@ __global__ __launch_bounds__(kThreads) void fp8bg_tiled(KArgs a) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[w][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    const int c0 = ((lane >> 4) * 2) ^ (lane & 7);
+    // operand rows are 16-aligned bases + (lane & 15), so swz(row) = swz(lane & 15)
+    const int c0 = ((lane >> 4) * 2) ^ swz(lane & 15, a.swz);
     auto opread = [&](int buf, int row) -> i32x8 {
         const unsigned char* base = lds + buf * BUF + row * kRowBytes;
         const i32x4 lo = *(const i32x4*)(base + (c0 << 4));
@@ -358,10 +374,10 @@ __device__ __forceinline__ void wait_vmcnt_lds() {
 // of the stacked [weights; tokens] tile (TW + TT rows of 128 bytes) is copied
 // global -> LDS by global_load_lds_dwordx4: one instruction moves 64 lanes x
 // 16 bytes = 8 rows into a contiguous 1 KB block, lane l writing chunk slot
-// l % 8 of row l / 8.  The lane fetches global chunk (l % 8) ^ (row % 8), so
-// chunk c of a row sits at slot c ^ (row % 8): the XOR swizzle that keeps the
-// MFMA operand reads (8 consecutive lanes = 8 consecutive rows, same chunk)
-// on distinct banks.  The group's scales travel the same way: one
+// l % 8 of row l / 8.  The lane fetches global chunk (l % 8) ^ swz(row), so
+// chunk c of a row sits at slot c ^ swz(row): the XOR swizzle that spreads
+// the MFMA operand reads (16 consecutive lanes = 16 consecutive rows, same
+// chunk) over the LDS banks.  The group's scales travel the same way: one
 // global_load_lds_dword per wave fills a 64-float slice of the stage's scale
 // area with the tile's As column (slots 0 .. TT-1) and its Bs values (slots
 // TT .. TT + TW/128 - 1).  ST stages form a ring: the loads of group
@@ -421,7 +437,7 @@ __global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
     for (int j = 0; j < NJ; ++j) {
         const int b = wave * NJ + j;
         const int row = 8 * b + (lane >> 3);
-        const int chunk = (lane & 7) ^ (row & 7);
+        const int chunk = (lane & 7) ^ swz(row, a.swz);
         if (8 * b < TW) {
             sbase[j] = a.B;
             soff[j] = (uint32_t)min(w0 + row, a.N - 1) * (uint32_t)a.K + chunk * 16;
@@ -463,7 +479,7 @@ __global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[w][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    const int c0 = ((lane >> 4) * 2) ^ (lane & 7);
+    const int c0 = ((lane >> 4) * 2) ^ swz(lane & 15, a.swz);
     auto opread = [&](const unsigned char* st, int row) -> i32x8 {
         const unsigned char* base = st + row * kRowBytes;
         const i32x4 lo = *(const i32x4*)(base + (c0 << 4));
@@ -485,6 +501,7 @@ __global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
         // Stage i is complete once at most the DMA instructions of the ST - 2
         // later steps are outstanding (vmcnt retires in issue order); this
         // wave's LDS reads of stage (i - 1) % ST have all returned.
+        __builtin_amdgcn_s_setprio(0);
         wait_vmcnt_lds<NDMA * (ST - 2)>();
         // All waves' blocks of stage i have landed, and every wave is done
         // reading stage (i - 1) % ST, which is refilled next.  The empty asm
@@ -494,6 +511,9 @@ __global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         dma(min(k_lo + i + ST - 1, g_last), (i + ST - 1) % ST);
+        // Raised wave priority while this wave's MFMA stream is issued, so a
+        // SIMD's two waves keep the matrix pipe fed ahead of memory issue.
+        __builtin_amdgcn_s_setprio(1);
 
         const unsigned char* st = lds + (i % ST) * STAGE;
         const float* sc = (const float*)(st + OPS);
@@ -509,6 +529,7 @@ __global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
             for (int w = 0; w < NW; ++w) promote(acc[w][t], mfma16x16x128(wop[w], top), s_t);
         }
     }
+    __builtin_amdgcn_s_setprio(0);
     // The clamped loads of the last ST - 1 steps are still in flight: they
     // must land before the workgroup's LDS can be handed to another one.
     wait_vmcnt<0>();
@@ -822,7 +843,10 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     if (ki < 0) return FP8BG_ERR_CONFIG;
     if (cfg->split < 1 || cfg->group_t < 1 || num_cus < 1) return FP8BG_ERR_CONFIG;
     if (cfg->split_mode < FP8BG_SPLIT_NONE || cfg->split_mode > FP8BG_SPLIT_FULL) return FP8BG_ERR_CONFIG;
-    if (cfg->flags & ~(FP8BG_FLAG_SCALE_LDS | FP8BG_FLAG_XCD_REMAP)) return FP8BG_ERR_CONFIG;
+    if (cfg->flags & ~(FP8BG_FLAG_SCALE_LDS | FP8BG_FLAG_XCD_REMAP | FP8BG_FLAG_SWZ8 |
+                       FP8BG_FLAG_SWZPAIR))
+        return FP8BG_ERR_CONFIG;
+    if ((cfg->flags & FP8BG_FLAG_SWZ8) && (cfg->flags & FP8BG_FLAG_SWZPAIR)) return FP8BG_ERR_CONFIG;
     const int kg = K / 128;
     const Instance& k = kInstances[ki];
     if (k.kf && kg != k.kf) return FP8BG_ERR_CONFIG;
@@ -906,6 +930,7 @@ int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_
     a.group_t = cfg->group_t;
     a.xcd_remap = (cfg->flags & FP8BG_FLAG_XCD_REMAP) ? 1 : 0;
     a.scale_lds = (cfg->flags & FP8BG_FLAG_SCALE_LDS) ? 1 : 0;
+    a.swz = (cfg->flags & FP8BG_FLAG_SWZ8) ? 1 : (cfg->flags & FP8BG_FLAG_SWZPAIR) ? 2 : 0;
     const size_t shm = a.scale_lds ? (size_t)k.tt * (K / 128) * sizeof(float) : 0;
     hipStream_t s = (hipStream_t)stream;
     k.launch(dim3(p.grid), shm, s, a);

@@ -11,11 +11,12 @@ Two families of config dicts are accepted:
 
 * gfx950-native entries written by this package's tuner:
   - impl "tiled": BLOCK_W, BLOCK_T, WAVES_W, WAVES_T, SPLIT, SPLIT_MODE,
-    GROUP_SIZE_M, SCALE_LDS, XCD_REMAP (LDS-tiled kernel);
+    GROUP_SIZE_M, SCALE_LDS, XCD_REMAP, LDS_SWIZZLE (LDS-tiled kernel);
   - impl "skinny": BLOCK_W, BLOCK_T, WAVES_K, UNROLL, SPLIT, SPLIT_MODE,
     XCD_REMAP (small-M kernel, waves split K);
   - impl "ring": BLOCK_W, BLOCK_T, WAVES_W, WAVES_T, STAGES, SPLIT,
-    SPLIT_MODE, GROUP_SIZE_M, XCD_REMAP (direct-to-LDS ring kernel);
+    SPLIT_MODE, GROUP_SIZE_M, XCD_REMAP, LDS_SWIZZLE (direct-to-LDS ring
+    kernel);
   - impl "shortk": BLOCK_W, BLOCK_T (K == 256, no K loop).
 * the reference's H20 entries (impl "triton", "gluon", "v2", "scale_tma",
   "shortk" with BM/BN keys), translated onto the nearest compiled gfx950 tile
@@ -105,6 +106,10 @@ def _flags(cfg):
         flags |= _lib.FLAG_SCALE_LDS
     if cfg.get("XCD_REMAP", False):
         flags |= _lib.FLAG_XCD_REMAP
+    swz = cfg.get("LDS_SWIZZLE", "row16")
+    if swz not in ("row8", "row16", "pair"):
+        raise ValueError("LDS_SWIZZLE must be one of ('row8', 'row16', 'pair')")
+    flags |= {"row16": 0, "row8": _lib.FLAG_SWZ8, "pair": _lib.FLAG_SWZPAIR}[swz]
     return flags
 
 

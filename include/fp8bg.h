@@ -80,6 +80,11 @@ extern "C" {
 #define FP8BG_FLAG_SCALE_LDS 0x1
 /* Remap workgroup ids so that consecutive tiles run on the same XCD (L2). */
 #define FP8BG_FLAG_XCD_REMAP 0x2
+/* LDS chunk swizzle of the tiled and ring kernels (chunk c of row r is stored
+ * at slot c ^ swz(r)); default swz = (r & 7) ^ ((r >> 3) & 1), free of bank
+ * conflicts for the MFMA operand reads.  At most one of: */
+#define FP8BG_FLAG_SWZ8      0x4   /* swz = r & 7 */
+#define FP8BG_FLAG_SWZPAIR   0x8   /* swz = (r >> 1) & 7 */
 
 /*
  * Kernel configuration: one gfx950 table entry (fp8_gemm_h20_amd/configs/*.json).
