@@ -42,6 +42,8 @@ EXPORTS = (
     "fp8bg_make_plan",
     "fp8bg_config_supported",
     "fp8bg_gemm",
+    "fp8bg_quant_act",
+    "fp8bg_e4m3_encode_host",
     "fp8bg_strerror",
 )
 
@@ -115,6 +117,10 @@ def _declare(lib):
         vp,                     # stream
     ]
     lib.fp8bg_gemm.restype = ctypes.c_int
+    lib.fp8bg_quant_act.argtypes = [vp, i64, vp, vp, i64, i64, i32, i32, ctypes.c_float, vp]
+    lib.fp8bg_quant_act.restype = ctypes.c_int
+    lib.fp8bg_e4m3_encode_host.argtypes = [vp, vp, i64]
+    lib.fp8bg_e4m3_encode_host.restype = ctypes.c_int
     lib.fp8bg_strerror.argtypes = [ctypes.c_int]
     lib.fp8bg_strerror.restype = ctypes.c_char_p
 

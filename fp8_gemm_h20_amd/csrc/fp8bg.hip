@@ -706,6 +706,76 @@ __global__ __launch_bounds__(kThreads) void fp8bg_split_reduce(KArgs a, int skin
     }
 }
 
+// ===========================================================================
+// Per-token-group activation quantisation (bf16 -> e4m3 + fp32 scale)
+// ===========================================================================
+// fp32 -> OCP e4m3 ("fn") code, round to nearest even, matching torch's
+// float -> float8_e4m3fn cast: NaN and |x| >= 480 (which would round past the
+// largest finite 448) give 0x7f with the sign; subnormals are multiples of
+// 2^-9.  Pure integer/float arithmetic, identical on host and device.
+__host__ __device__ inline uint32_t e4m3_from_f32(float f) {
+    uint32_t u;
+    __builtin_memcpy(&u, &f, 4);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    u &= 0x7fffffffu;
+    if (u >= 0x43f00000u) return sign | 0x7fu;          // NaN, inf, |x| >= 480
+    if (u < 0x3c800000u) {                               // |x| < 2^-6: subnormal grid
+        float a;
+        __builtin_memcpy(&a, &u, 4);
+        return sign | (uint32_t)__builtin_rintf(a * 512.0f);   // 0 .. 8 (8 = 2^-6)
+    }
+    const uint32_t r = u + 0x7ffffu + ((u >> 20) & 1u);  // RNE to 3 mantissa bits
+    return sign | ((((r >> 23) - 120u) << 3) | ((r >> 20) & 7u));
+}
+
+struct QArgs {
+    const uint16_t* x;     // bf16 [M, K], row stride ldx elements
+    uint8_t* q;            // e4m3 [M, K], row stride K
+    float* s;              // fp32 [M, K/128], strides s_sm, s_sk
+    int64_t ldx, s_sm, s_sk;
+    int M, K;
+    float eps;
+};
+
+// 16 lanes per 128-element group, 8 elements (16 bytes) per lane.
+__global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
+    const int kg = a.K / kGroupK;
+    const int64_t group = (int64_t)blockIdx.x * (kThreads / 16) + (threadIdx.x >> 4);
+    const int sub = threadIdx.x & 15;
+    if (group >= (int64_t)a.M * kg) return;              // whole 16-lane groups exit together
+    const int m = (int)(group / kg), g = (int)(group % kg);
+    const int col = g * kGroupK + sub * 8;
+    const i32x4 raw = *(const i32x4*)(a.x + m * a.ldx + col);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float((uint32_t)raw[i] << 16);
+        v[2 * i + 1] = __uint_as_float((uint32_t)raw[i] & 0xffff0000u);
+    }
+    // amax with NaN propagation (a NaN anywhere in the group makes its scale
+    // NaN, as max/clamp do in the reference recipe)
+    float amax = 0.f;
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        nan |= __builtin_isnan(v[i]);
+    }
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, d, 16));
+        nan |= __shfl_xor((int)nan, d, 16) != 0;
+    }
+    const float scale = nan ? __builtin_nanf("") : fmaxf(amax, a.eps) / 448.0f;
+    uint2 o;
+    o.x = e4m3_from_f32(v[0] / scale) | (e4m3_from_f32(v[1] / scale) << 8) |
+          (e4m3_from_f32(v[2] / scale) << 16) | (e4m3_from_f32(v[3] / scale) << 24);
+    o.y = e4m3_from_f32(v[4] / scale) | (e4m3_from_f32(v[5] / scale) << 8) |
+          (e4m3_from_f32(v[6] / scale) << 16) | (e4m3_from_f32(v[7] / scale) << 24);
+    *(uint2*)(a.q + (int64_t)m * a.K + col) = o;
+    if (sub == 0) a.s[m * a.s_sm + g * a.s_sk] = scale;
+}
+
 // ---------------------------------------------------------------------------
 // Compiled instances
 // ---------------------------------------------------------------------------
@@ -940,6 +1010,38 @@ int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_
                            k.kind == FP8BG_KIND_SKINNY ? 1 : 0);
         if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
     }
+    return FP8BG_OK;
+}
+
+int fp8bg_quant_act(const void* x, int64_t x_stride_m, void* q, float* s, int64_t s_stride_m,
+                    int64_t s_stride_k, int32_t M, int32_t K, float eps, void* stream) {
+    if (!x || !q || !s) return FP8BG_ERR_NULL;
+    if (M < 1 || K < 128 || K % 128 || x_stride_m < K) return FP8BG_ERR_SHAPE;
+    if (!(eps > 0.f) || !(eps < 3.4e38f)) return FP8BG_ERR_CONFIG;
+    // 16-byte loads of x rows and 8-byte stores of q
+    if ((((uintptr_t)x) & 15) || (x_stride_m % 8) || (((uintptr_t)q) & 7) || (((uintptr_t)s) & 3))
+        return FP8BG_ERR_ALIGN;
+    const int64_t groups = (int64_t)M * (K / 128);
+    const int64_t blocks = (groups + kThreads / 16 - 1) / (kThreads / 16);
+    if (blocks > 0x7fffffff) return FP8BG_ERR_SHAPE;
+    QArgs a;
+    a.x = (const uint16_t*)x;
+    a.q = (uint8_t*)q;
+    a.s = s;
+    a.ldx = x_stride_m;
+    a.s_sm = s_stride_m;
+    a.s_sk = s_stride_k;
+    a.M = M;
+    a.K = K;
+    a.eps = eps;
+    hipLaunchKernelGGL(fp8bg_quant_act_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
+                       (hipStream_t)stream, a);
+    return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
+}
+
+int fp8bg_e4m3_encode_host(const float* x, uint8_t* out, int64_t n) {
+    if (!x || !out || n < 0) return FP8BG_ERR_NULL;
+    for (int64_t i = 0; i < n; ++i) out[i] = (uint8_t)e4m3_from_f32(x[i]);
     return FP8BG_OK;
 }
 

@@ -31,3 +31,48 @@ def matmul(A, B, As, Bs, *, profile="35b_tp1"):
     entry, _ = _select(profile, m, n, k)
     with torch.cuda.device(A.device):
         return run(entry, (A, B, As, Bs))
+
+
+def quantize_act(x, *, eps=1e-10, column_major_scales=False):
+    """bf16 x[..., K] -> (e4m3 q[M, K], fp32 s[M, K/128]) per 1x128 K group on x's GPU.
+
+    s = max(amax(group), eps) / 448 and q = e4m3(x / s) with round to
+    nearest even: the operands the reference's SGLang adapter feeds to
+    matmul after sglang_per_token_group_quant_fp8 (eps=1e-10 default there;
+    sgl_patch/fp8mm_sglang_patch.py:51-53).  Leading dims of x are flattened
+    into M.  column_major_scales=True returns s as the transposed view of a
+    [K/128, M] buffer (same values).  One HIP kernel, no host sync.
+    """
+    import torch
+    from . import kernels
+    if x.dtype != torch.bfloat16 or not x.is_cuda:
+        raise ValueError("x must be a bfloat16 CUDA tensor")
+    k = x.shape[-1]
+    if k % 128:
+        raise ValueError("K must be a multiple of 128")
+    x2 = x.reshape(-1, k)
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.clone(memory_format=torch.contiguous_format)    # kernel reads 16-byte row chunks
+    m = x2.shape[0]
+    if m < 1:
+        raise ValueError("x must have at least one row")
+    with torch.cuda.device(x.device):
+        return kernels.quant_act(x2, m, k, eps, column_major_scales)
+
+
+def linear(x, B, Bs, *, profile="35b_tp1", bias=None, eps=1e-10):
+    """y = x @ dequant(B, Bs)^T (+ bias) for bf16 activations x[..., K].
+
+    The dense block-FP8 linear of the reference's SGLang adapter
+    (fp8mm_w8a8_block_fp8_linear, sgl_patch/fp8mm_sglang_patch.py:34-57):
+    per-token-group quantisation of x, matmul, then `out + bias` in bf16, and
+    the result viewed as x.shape[:-1] + (N,).  Shapes the profile does not
+    cover raise ValueError (the adapter's own fallback decision stays with
+    the caller, as `supports` answers it).
+    """
+    n, k = B.shape
+    q, s = quantize_act(x, eps=eps)
+    out = matmul(q, B, s, Bs, profile=profile)
+    if bias is not None:
+        out = out + bias
+    return out.view(*x.shape[:-1], n)

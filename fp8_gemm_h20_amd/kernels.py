@@ -239,6 +239,21 @@ def launch(A, B, As, Bs, cstruct):
     return C
 
 
+def quant_act(x2, m, k, eps, column_major_scales):
+    """Launch the activation quantiser on a [M, K] bf16 view (unit column stride)."""
+    import torch
+    dev = x2.device
+    q = torch.empty((m, k), device=dev, dtype=torch.float8_e4m3fn)
+    if column_major_scales:
+        s = torch.empty((k // 128, m), device=dev, dtype=torch.float32).T
+    else:
+        s = torch.empty((m, k // 128), device=dev, dtype=torch.float32)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    _lib.check(_lib.lib().fp8bg_quant_act(x2.data_ptr(), x2.stride(0), q.data_ptr(), s.data_ptr(),
+                                          s.stride(0), s.stride(1), m, k, ctypes.c_float(eps), stream))
+    return q, s
+
+
 def _freeze(config):
     return tuple(sorted(config.items()))
 

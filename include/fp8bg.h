@@ -170,6 +170,32 @@ int fp8bg_gemm(const void* A, const void* B,
                float* ws, int64_t ws_elems,
                void* stream);
 
+/*
+ * Per-token-group activation quantisation (stream-ordered, no sync):
+ *   for every row m and 128-wide K group g of x (bf16 [M,K], row stride
+ *   x_stride_m elements, a multiple of 8; 16-byte aligned):
+ *     s[m,g] = max(max_k |x[m,k]|, eps) / 448            (fp32, IEEE division)
+ *     q[m,k] = e4m3(x[m,k] / s[m,g])                      (round to nearest even)
+ *   q is e4m3 [M,K] row-major (row stride K); s is fp32 [M,K/128] with element
+ *   strides (s_stride_m, s_stride_k), so row-major (K/128, 1) and column-major
+ *   (1, M) scales are both direct outputs.
+ * Produces the operands that the reference's SGLang adapter obtains from
+ * sglang_per_token_group_quant_fp8(x, 128, column_major_scales=False,
+ * scale_tma_aligned=False) before calling matmul
+ * (sgl_patch/fp8mm_sglang_patch.py:51-54); same formula as the reference's
+ * test recipe (scripts/validate.py:26-29, clamp_min(eps) then / 448).
+ */
+int fp8bg_quant_act(const void* x, int64_t x_stride_m, void* q,
+                    float* s, int64_t s_stride_m, int64_t s_stride_k,
+                    int32_t M, int32_t K, float eps, void* stream);
+
+/*
+ * Host copy of the kernels' fp32 -> e4m3 conversion (round to nearest even,
+ * NaN/|x| >= 480 -> 0x7f|sign), for host-side checks of that arithmetic.
+ * No reference counterpart (the reference relies on torch's cast).
+ */
+int fp8bg_e4m3_encode_host(const float* x, uint8_t* out, int64_t n);
+
 /* Static message for an error code. */
 const char* fp8bg_strerror(int code);
 

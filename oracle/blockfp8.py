@@ -33,7 +33,8 @@ def e4m3_encode(x):
     """float32 -> e4m3fn codes, round to nearest even.
 
     Matches torch's float -> float8_e4m3fn cast: results above 448 after
-    rounding (|x| > 464) become NaN (0x7F with the sign), NaN stays NaN.
+    rounding (|x| > 464) and +-inf become NaN (0x7F with the sign), NaN stays
+    NaN.
     """
     x = np.asarray(x, dtype=np.float32)
     a = np.abs(x).astype(np.float64)
@@ -42,9 +43,10 @@ def e4m3_encode(x):
         e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
     e = np.maximum(e, -6.0)                       # subnormals share the 2^-6 binade quantum
     quantum = np.exp2(e - 3.0)
-    q = np.rint(a / quantum) * quantum            # rint = round half to even
+    with np.errstate(invalid="ignore"):
+        q = np.rint(a / quantum) * quantum        # rint = round half to even
     out = np.zeros(x.shape, dtype=np.uint8)
-    nan = np.isnan(x) | (q > E4M3_MAX)
+    nan = np.isnan(x) | np.isinf(x) | ~(q <= E4M3_MAX)
     sub = (q > 0) & (q < 2.0 ** -6) & ~nan
     out[sub] = np.rint(q[sub] / 2.0 ** -9).astype(np.uint8)
     nrm = (q >= 2.0 ** -6) & ~nan

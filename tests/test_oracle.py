@@ -49,7 +49,8 @@ def test_e4m3_encode_matches_torch_on_dense_sweep_and_ties():
         d, mids.astype(np.float32),
         np.nextafter(mids.astype(np.float32), np.float32(np.inf)),
         np.nextafter(mids.astype(np.float32), np.float32(-np.inf)),
-        np.float32([464, 465, 463.99, 480, 1e6, -464, 2 ** -10, 3 * 2 ** -11, 2 ** -11, -0.0, 0.0]),
+        np.float32([464, 465, 463.99, 480, 1e6, -464, 2 ** -10, 3 * 2 ** -11, 2 ** -11, -0.0, 0.0,
+                    np.inf, -np.inf, 3.4e38, -3.4e38]),
     ]).astype(np.float32)
     ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
     assert np.array_equal(ob.e4m3_encode(x), ref)
