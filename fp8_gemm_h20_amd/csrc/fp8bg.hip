@@ -385,7 +385,9 @@ __device__ __forceinline__ void wait_vmcnt_lds() {
 // and no VGPR-destination memory loads in the loop, and each group needs one
 // barrier.
 template <int TW, int TT, int WW, int WT, int ST, int KF>
-__global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
+__global__ __launch_bounds__(64 * WW * WT)
+__attribute__((amdgpu_waves_per_eu((WW * WT + 3) / 4, (WW * WT + 3) / 4)))
+void fp8bg_ring(KArgs a) {
     constexpr int NWAVE = WW * WT;
     constexpr int WTW = TW / WW;
     constexpr int WTT = TT / WT;
@@ -521,13 +523,41 @@ __global__ __launch_bounds__(64 * WW * WT) void fp8bg_ring(KArgs a) {
         i32x8 wop[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) wop[w] = opread(st, wv_w * WTW + w * 16 + (lane & 15));
+        // Software pipeline over token blocks: block t's products go into
+        // their own registers, and each MFMA is followed by the four
+        // promotion FMAs of the previous block's product for the same weight
+        // block, which run on the VALU while the MFMA occupies the matrix
+        // pipe; block t + 1's operand is read from LDS one block ahead.  The
+        // scheduling fences keep this order (the default schedule promotes
+        // each product right after its own MFMA and stalls on it).
+        i32x8 top = opread(st, TW + wv_t * WTT + (lane & 15));
+        float sa_t = sc[wv_t * WTT + (lane & 15)];
+        f32x4 prev[NW];
+        float s_prev = 0.f;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const float s_t = sc[wv_t * WTT + t * 16 + (lane & 15)] * sb;
-            const i32x8 top = opread(st, TW + wv_t * WTT + t * 16 + (lane & 15));
+            i32x8 top_next = top;
+            float sa_next = sa_t;
+            if (t + 1 < NT) {
+                top_next = opread(st, TW + wv_t * WTT + (t + 1) * 16 + (lane & 15));
+                sa_next = sc[wv_t * WTT + (t + 1) * 16 + (lane & 15)];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            f32x4 cur[NW];
 #pragma unroll
-            for (int w = 0; w < NW; ++w) promote(acc[w][t], mfma16x16x128(wop[w], top), s_t);
+            for (int w = 0; w < NW; ++w) {
+                cur[w] = mfma16x16x128(wop[w], top);
+                if (t > 0) promote(acc[w][t - 1], prev[w], s_prev);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int w = 0; w < NW; ++w) prev[w] = cur[w];
+            s_prev = sa_t * sb;
+            top = top_next;
+            sa_t = sa_next;
         }
+#pragma unroll
+        for (int w = 0; w < NW; ++w) promote(acc[w][NT - 1], prev[w], s_prev);
     }
     __builtin_amdgcn_s_setprio(0);
     // The clamped loads of the last ST - 1 steps are still in flight: they
