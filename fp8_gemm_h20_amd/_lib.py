@@ -11,7 +11,7 @@ from pathlib import Path
 
 LIB_NAME = "libfp8bg.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK = 0
 ERR_SHAPE = 1
@@ -111,6 +111,7 @@ def _declare(lib):
         vp, vp,                 # A, B
         vp, i64, i64,           # As, strides
         vp, i64, i64,           # Bs, strides
+        vp,                     # bias (bf16 [N] or NULL)
         vp, i32, i32, i32,      # C, M, N, K
         ctypes.POINTER(Config), i32,
         vp, i64,                # ws, ws_elems

@@ -63,6 +63,7 @@ struct KArgs {
     const float* As;       // [M, K/128]
     const float* Bs;       // [N/128, K/128]
     uint16_t* C;           // [M, N] bf16, row stride N
+    const uint16_t* bias;  // [N] bf16 or nullptr
     float* ws;             // split-K partials [split tile][split][tt][tw]
     int64_t as_sm, as_sk, bs_sn, bs_sk;
     int M, N, K;
@@ -89,6 +90,20 @@ __device__ __forceinline__ uint2 pack_bf16x4(const f32x4& v) {
     o.x = bf16_bits(v[0]) | (bf16_bits(v[1]) << 16);
     o.y = bf16_bits(v[2]) | (bf16_bits(v[3]) << 16);
     return o;
+}
+
+// bf16 output of four consecutive columns n .. n+3, with the optional bias
+// added the way a separate bf16 `C + bias` does it: C is rounded to bf16
+// first, then bf16(C) + bias is evaluated in fp32 and rounded again.
+__device__ __forceinline__ uint2 out_bf16x4(const f32x4& v, const uint16_t* bias, int n) {
+    if (!bias) return pack_bf16x4(v);
+    const uint2 b = *(const uint2*)(bias + n);
+    const uint32_t bb[4] = {b.x & 0xffffu, b.x >> 16, b.y & 0xffffu, b.y >> 16};
+    f32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        r[i] = __uint_as_float(bf16_bits(v[i]) << 16) + __uint_as_float(bb[i] << 16);
+    return pack_bf16x4(r);
 }
 
 __device__ __forceinline__ f32x4 mfma16x16x128(const i32x8& w, const i32x8& t) {
@@ -331,7 +346,7 @@ __global__ __launch_bounds__(kThreads) void fp8bg_tiled(KArgs a) {
             for (int w = 0; w < NW; ++w) {
                 const int n = w0 + wv_w * WTW + w * 16 + (lane >> 4) * 4;
                 if (n >= a.N) continue;
-                *(uint2*)(a.C + (size_t)m * a.N + n) = pack_bf16x4(acc[w][t]);
+                *(uint2*)(a.C + (size_t)m * a.N + n) = out_bf16x4(acc[w][t], a.bias, n);
             }
         }
         return;
@@ -574,7 +589,7 @@ void fp8bg_ring(KArgs a) {
             for (int w = 0; w < NW; ++w) {
                 const int n = w0 + wv_w * WTW + w * 16 + (lane >> 4) * 4;
                 if (n >= a.N) continue;
-                *(uint2*)(a.C + (size_t)m * a.N + n) = pack_bf16x4(acc[w][t]);
+                *(uint2*)(a.C + (size_t)m * a.N + n) = out_bf16x4(acc[w][t], a.bias, n);
             }
         }
         return;
@@ -701,7 +716,7 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
             *(f32x4*)(mine + tl * TW + wl) = s;
         } else {
             const int m = t0 + tl, n = w0 + wl;
-            if (m < a.M && n < a.N) *(uint2*)(a.C + (size_t)m * a.N + n) = pack_bf16x4(s);
+            if (m < a.M && n < a.N) *(uint2*)(a.C + (size_t)m * a.N + n) = out_bf16x4(s, a.bias, n);
         }
     }
 }
@@ -732,7 +747,7 @@ __global__ __launch_bounds__(kThreads) void fp8bg_split_reduce(KArgs a, int skin
             s[2] += v[2];
             s[3] += v[3];
         }
-        *(uint2*)(a.C + (size_t)m * a.N + n) = pack_bf16x4(s);
+        *(uint2*)(a.C + (size_t)m * a.N + n) = out_bf16x4(s, a.bias, n);
     }
 }
 
@@ -996,9 +1011,11 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
 
 int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_m,
                int64_t as_stride_k, const float* Bs, int64_t bs_stride_n, int64_t bs_stride_k,
-               void* C, int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg,
-               int32_t num_cus, float* ws, int64_t ws_elems, void* stream) {
+               const void* bias, void* C, int32_t M, int32_t N, int32_t K,
+               const fp8bg_config* cfg, int32_t num_cus, float* ws, int64_t ws_elems,
+               void* stream) {
     if (!A || !B || !As || !Bs || !C) return FP8BG_ERR_NULL;
+    if (((uintptr_t)bias) & 7) return FP8BG_ERR_ALIGN;
     fp8bg_plan p;
     const int rc = fp8bg_make_plan(M, N, K, cfg, num_cus, &p);
     if (rc != FP8BG_OK) return rc;
@@ -1013,6 +1030,7 @@ int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_
     a.As = As;
     a.Bs = Bs;
     a.C = (uint16_t*)C;
+    a.bias = (const uint16_t*)bias;
     a.ws = ws;
     a.as_sm = as_stride_m;
     a.as_sk = as_stride_k;

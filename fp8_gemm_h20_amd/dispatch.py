@@ -3,13 +3,19 @@ from .config import _select
 from .engine import run
 
 
-def matmul(A, B, As, Bs, *, profile="35b_tp1"):
+def matmul(A, B, As, Bs, *, profile="35b_tp1", bias=None, out=None):
     """FP8 A[M,K], B[N,K] with fp32 block scales -> bf16 C[M,N] on A's device.
 
     Checks run in the reference's order and raise ValueError with its
     messages (dispatch.py:12-27); scale strides are not restricted.  Shapes
     outside the profile and M outside 1..16384 raise ValueError.  There is
     no fallback: the gfx950 HIP library must be built.
+
+    Additions to the reference signature (defaults keep its behaviour):
+    `bias` - bf16 [N] added in the kernel epilogue, bit-identical to a
+    separate bf16 `C + bias` (the adapter's sgl_patch/fp8mm_sglang_patch.py:55-56);
+    `out` - a contiguous bf16 [M, N] tensor on A's device to write into
+    instead of allocating C (returned).
     """
     import torch
     if A.ndim != 2 or B.ndim != 2:
@@ -28,9 +34,17 @@ def matmul(A, B, As, Bs, *, profile="35b_tp1"):
         raise ValueError("Scales must be float32")
     if tuple(As.shape) != (m, k // 128) or tuple(Bs.shape) != (n // 128, k // 128):
         raise ValueError("Expected As[M,K/128] and Bs[N/128,K/128]")
+    if bias is not None and (bias.dtype != torch.bfloat16 or tuple(bias.shape) != (n,)
+                             or bias.device != A.device or not bias.is_contiguous()):
+        raise ValueError("bias must be a contiguous bfloat16 [N] tensor on A's device")
+    if out is not None and (out.dtype != torch.bfloat16 or tuple(out.shape) != (m, n)
+                            or out.device != A.device or not out.is_contiguous()):
+        raise ValueError("out must be a contiguous bfloat16 [M, N] tensor on A's device")
     entry, _ = _select(profile, m, n, k)
     with torch.cuda.device(A.device):
-        return run(entry, (A, B, As, Bs))
+        if bias is None and out is None:
+            return run(entry, (A, B, As, Bs))
+        return run(entry, (A, B, As, Bs), bias=bias, out=out)
 
 
 def quantize_act(x, *, eps=1e-10, column_major_scales=False):
@@ -65,14 +79,13 @@ def linear(x, B, Bs, *, profile="35b_tp1", bias=None, eps=1e-10):
 
     The dense block-FP8 linear of the reference's SGLang adapter
     (fp8mm_w8a8_block_fp8_linear, sgl_patch/fp8mm_sglang_patch.py:34-57):
-    per-token-group quantisation of x, matmul, then `out + bias` in bf16, and
-    the result viewed as x.shape[:-1] + (N,).  Shapes the profile does not
-    cover raise ValueError (the adapter's own fallback decision stays with
-    the caller, as `supports` answers it).
+    per-token-group quantisation of x, matmul with the bias added in the
+    kernel epilogue (bit-identical to the adapter's `out + bias`), and the
+    result viewed as x.shape[:-1] + (N,).  Two kernels, no host sync.  Shapes
+    the profile does not cover raise ValueError (the adapter's own fallback
+    decision stays with the caller, as `supports` answers it).
     """
     n, k = B.shape
     q, s = quantize_act(x, eps=eps)
-    out = matmul(q, B, s, Bs, profile=profile)
-    if bias is not None:
-        out = out + bias
+    out = matmul(q, B, s, Bs, profile=profile, bias=bias)
     return out.view(*x.shape[:-1], n)

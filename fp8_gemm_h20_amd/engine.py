@@ -37,5 +37,5 @@ def kernel(name):
     return getattr(import_module(f".{module}", __package__), function)
 
 
-def run(entry, args):
-    return kernel(entry["impl"])(*args, dict(entry["config"]))
+def run(entry, args, **epilogue):
+    return kernel(entry["impl"])(*args, dict(entry["config"]), **epilogue)

@@ -5,7 +5,9 @@ Each function keeps the reference's L0 wrapper contract
 As[M,K/128] and Bs[N/128,K/128] fp32 with any strides, `config` a plain dict;
 it allocates C = empty(M, N, bf16) on A's device, enqueues the HIP kernel(s)
 on the current stream through the C ABI (include/fp8bg.h) and returns C
-without synchronising.
+without synchronising.  Optional keywords (beyond the reference contract):
+`bias` (bf16 [N], added in the epilogue like a separate bf16 `C + bias`) and
+`out` (a bf16 [M, N] contiguous buffer to write instead of allocating).
 
 Two families of config dicts are accepted:
 
@@ -216,15 +218,16 @@ def _workspace(dev, ws_elems):
     return bufs.get(ws_elems)
 
 
-def launch(A, B, As, Bs, cstruct):
-    """Allocate C and enqueue the kernel(s) described by `cstruct`."""
+def launch(A, B, As, Bs, cstruct, bias=None, out=None):
+    """Enqueue the kernel(s) described by `cstruct` into `out` (allocated
+    when None); `bias` is an optional bf16 [N] added in the epilogue."""
     import torch
     M, K = A.shape
     N = B.shape[0]
     dev = A.device
     cus = num_cus(dev)
     plan = _lib.make_plan(M, N, K, cstruct, cus)
-    C = torch.empty((M, N), device=dev, dtype=torch.bfloat16)
+    C = torch.empty((M, N), device=dev, dtype=torch.bfloat16) if out is None else out
     ws_ptr, ws_n = None, 0
     if plan.n_split:
         ws = _workspace(dev, plan.ws_elems)
@@ -234,6 +237,7 @@ def launch(A, B, As, Bs, cstruct):
         A.data_ptr(), B.data_ptr(),
         As.data_ptr(), As.stride(0), As.stride(1),
         Bs.data_ptr(), Bs.stride(0), Bs.stride(1),
+        None if bias is None else bias.data_ptr(),
         C.data_ptr(), M, N, K, ctypes.byref(cstruct), cus,
         ws_ptr, ws_n, stream))
     return C
@@ -276,23 +280,24 @@ def _ring_cached(items, k_fixed):
 # ---------------------------------------------------------------------------
 # gfx950-native impls
 # ---------------------------------------------------------------------------
-def tiled(A, B, As, Bs, config):
+def tiled(A, B, As, Bs, config, **epilogue):
     """LDS-tiled MFMA kernel with optional tail/full split-K."""
-    return launch(A, B, As, Bs, _tiled_cached(_freeze(config), 0))
+    return launch(A, B, As, Bs, _tiled_cached(_freeze(config), 0), **epilogue)
 
 
-def skinny(A, B, As, Bs, config):
+def skinny(A, B, As, Bs, config, **epilogue):
     """Small-M kernel: operands straight to registers, waves split K."""
-    return launch(A, B, As, Bs, _skinny_cached(_freeze(config)))
+    return launch(A, B, As, Bs, _skinny_cached(_freeze(config)), **epilogue)
 
 
-def ring(A, B, As, Bs, config):
+def ring(A, B, As, Bs, config, **epilogue):
     """Large-tile kernel: direct-to-LDS ring, one barrier per K group.
     K_FIXED=2 selects the K == 256 instance with both groups unrolled."""
-    return launch(A, B, As, Bs, _ring_cached(_freeze(config), int(config.get("K_FIXED", 0))))
+    return launch(A, B, As, Bs, _ring_cached(_freeze(config), int(config.get("K_FIXED", 0))),
+                  **epilogue)
 
 
-def shortk(A, B, As, Bs, config):
+def shortk(A, B, As, Bs, config, **epilogue):
     """K == 256 kernel: both scale groups unrolled, no K loop, no split-K.
 
     Accepts gfx950 keys (BLOCK_W/BLOCK_T) or the reference's shortk keys
@@ -303,7 +308,7 @@ def shortk(A, B, As, Bs, config):
     if "BLOCK_W" not in config:
         tw, tt = nearest_tile(int(config["BN"]), int(config["BM"]), k_fixed=2)
         config = {"BLOCK_W": tw, "BLOCK_T": tt, "GROUP_SIZE_M": int(config.get("GROUP", 1))}
-    return launch(A, B, As, Bs, _tiled_cached(_freeze(config), 2))
+    return launch(A, B, As, Bs, _tiled_cached(_freeze(config), 2), **epilogue)
 
 
 # earlier name of the tiled impl
@@ -320,30 +325,30 @@ def _compat(tw_req, tt_req, split, mode, group, scale_lds=False):
     return _tiled_cached(_freeze(cfg), 0)
 
 
-def triton(A, B, As, Bs, config):
+def triton(A, B, As, Bs, config, **epilogue):
     """Reference c3 entry (kernels/baseline_triton.py:87-114): full-grid split-K."""
     c = _compat(config["BLOCK_SIZE_N"], config["BLOCK_SIZE_M"], config.get("SPLIT_K", 1), "full",
                 config.get("GROUP_SIZE_M", 1))
-    return launch(A, B, As, Bs, c)
+    return launch(A, B, As, Bs, c, **epilogue)
 
 
-def gluon(A, B, As, Bs, config):
+def gluon(A, B, As, Bs, config, **epilogue):
     """Reference c11 entry (kernels/baseline_gluon.py:259-293): tail split-K."""
     c = _compat(config["BLOCK_W"], config["BLOCK_T"], config.get("SPLIT", 1), "tail",
                 config.get("GROUP_SIZE_M", 1))
-    return launch(A, B, As, Bs, c)
+    return launch(A, B, As, Bs, c, **epilogue)
 
 
-def v2(A, B, As, Bs, config):
+def v2(A, B, As, Bs, config, **epilogue):
     """Reference v2 entry (kernels/kernel_v2.py:339-376): same schedule as c11."""
-    return gluon(A, B, As, Bs, config)
+    return gluon(A, B, As, Bs, config, **epilogue)
 
 
-def scale_tma(A, B, As, Bs, config):
+def scale_tma(A, B, As, Bs, config, **epilogue):
     """Reference scale-TMA entry (kernels/kernel_scale_tma.py:356-396).
 
     Stages As in LDS when As is row-major, and otherwise runs the v2 path,
     mirroring the reference's `As.stride(1) != 1` fallback (:367-369)."""
     c = _compat(config["BLOCK_W"], config["BLOCK_T"], config.get("SPLIT", 1), "tail",
                 config.get("GROUP_SIZE_M", 1), scale_lds=As.stride(1) == 1)
-    return launch(A, B, As, Bs, c)
+    return launch(A, B, As, Bs, c, **epilogue)

@@ -40,7 +40,7 @@ extern "C" {
 
 /* ABI version returned by fp8bg_version(); bumped on any signature or struct
  * change. */
-#define FP8BG_ABI_VERSION 2
+#define FP8BG_ABI_VERSION 3
 
 /* ---- kernel kinds --------------------------------------------------------- */
 /* LDS-tiled kernel: a block_w x block_t workgroup tile, 4 waves in a
@@ -161,11 +161,15 @@ int fp8bg_config_supported(const fp8bg_config* cfg);
  * (same stream); a captured hipGraph keeps using the `ws` it was captured
  * with, so that buffer must outlive the graph.
  * Scale strides are in elements.  A, B and C must be 16-byte aligned.
+ * `bias` (bf16 [N], 8-byte aligned, or NULL) is added in the epilogue exactly
+ * as the reference adapter's separate `out + bias` does it
+ * (sgl_patch/fp8mm_sglang_patch.py:55-56): C is rounded to bf16, then
+ * bf16(C) + bias is evaluated in fp32 and rounded to bf16 again.
  */
 int fp8bg_gemm(const void* A, const void* B,
                const float* As, int64_t as_stride_m, int64_t as_stride_k,
                const float* Bs, int64_t bs_stride_n, int64_t bs_stride_k,
-               void* C, int32_t M, int32_t N, int32_t K,
+               const void* bias, void* C, int32_t M, int32_t N, int32_t K,
                const fp8bg_config* cfg, int32_t num_cus,
                float* ws, int64_t ws_elems,
                void* stream);
