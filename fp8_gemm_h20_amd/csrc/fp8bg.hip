@@ -55,6 +55,13 @@ constexpr int kThreads = 256;
 constexpr int kGroupK = 128;          // K elements per scale group
 constexpr int kRowBytes = kGroupK;    // one fp8 row of a group = 128 bytes
 constexpr int kMaxLds = 160 * 1024;   // gfx950 LDS per workgroup
+
+// Scale-area DMA instructions per wave and stage of the ring kernel: one
+// 64-dword slice per wave carries the tile's As column (tt floats), its Bs
+// blocks (ceil(tw / 128) floats) and the bias row (tw bf16 = tw / 2 dwords).
+constexpr int ring_scale_slices(int tw, int tt, int nwave) {
+    return (tt + (tw + 127) / 128 + tw / 2 + 64 * nwave - 1) / (64 * nwave);
+}
 constexpr int kNumXcd = 8;            // MI355X: 8 XCDs, workgroups dealt round-robin
 
 struct KArgs {
@@ -95,15 +102,19 @@ __device__ __forceinline__ uint2 pack_bf16x4(const f32x4& v) {
 // bf16 output of four consecutive columns n .. n+3, with the optional bias
 // added the way a separate bf16 `C + bias` does it: C is rounded to bf16
 // first, then bf16(C) + bias is evaluated in fp32 and rounded again.
-__device__ __forceinline__ uint2 out_bf16x4(const f32x4& v, const uint16_t* bias, int n) {
-    if (!bias) return pack_bf16x4(v);
-    const uint2 b = *(const uint2*)(bias + n);
+// (out_bf16x4v: the same with the four bias values b already in registers.)
+__device__ __forceinline__ uint2 out_bf16x4v(const f32x4& v, bool has_bias, uint2 b) {
+    if (!has_bias) return pack_bf16x4(v);
     const uint32_t bb[4] = {b.x & 0xffffu, b.x >> 16, b.y & 0xffffu, b.y >> 16};
     f32x4 r;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         r[i] = __uint_as_float(bf16_bits(v[i]) << 16) + __uint_as_float(bb[i] << 16);
     return pack_bf16x4(r);
+}
+
+__device__ __forceinline__ uint2 out_bf16x4(const f32x4& v, const uint16_t* bias, int n) {
+    return bias ? out_bf16x4v(v, true, *(const uint2*)(bias + n)) : pack_bf16x4(v);
 }
 
 __device__ __forceinline__ f32x4 mfma16x16x128(const i32x8& w, const i32x8& t) {
@@ -410,14 +421,19 @@ void fp8bg_ring(KArgs a) {
     constexpr int NT = WTT / 16;
     constexpr int ROWS = TW + TT;
     constexpr int NJ = ROWS / (8 * NWAVE);        // 1 KB operand blocks per wave per group
-    constexpr int NDMA = NJ + 1;                  // + one scale slice per wave
+    constexpr int NSC = ring_scale_slices(TW, TT, NWAVE);
+    constexpr int NDMA = NJ + NSC;                // + the scale slices
     constexpr int OPS = ROWS * kRowBytes;         // operand bytes per stage
-    constexpr int SCALES = NWAVE * 64;            // scale slots per stage
+    constexpr int SCALES = NSC * NWAVE * 64;      // scale slots per stage
     constexpr int STAGE = OPS + SCALES * 4;
     static_assert(WTW % 16 == 0 && WTT % 16 == 0 && NW >= 1 && NT >= 1, "wave tile");
     static_assert(ROWS % (8 * NWAVE) == 0 && NJ >= 1, "DMA blocks per wave");
     constexpr int NBS = (TW + 127) / 128;         // Bs blocks the tile spans
-    static_assert(TT + NBS <= SCALES, "scale slots");
+    static_assert(TT + NBS + TW / 2 <= SCALES, "scale slots");
+    // epilogue: 16 output rows of a wave at a time, staged in LDS
+    constexpr int ROWB = WTW * 2;                 // bf16 bytes of one wave row
+    constexpr int CPR = ROWB / 16;                // 16-byte chunks per wave row
+    static_assert(NWAVE * 16 * ROWB <= OPS, "epilogue slices inside stage 0's operands");
     static_assert(WTW <= 128 && 128 % WTW == 0, "wave weight rows inside one Bs block");
     static_assert(ST >= 2 && NDMA * (ST - 2) < 64, "ring depth");
     static_assert(ST * STAGE <= kMaxLds, "LDS");
@@ -463,21 +479,29 @@ void fp8bg_ring(KArgs a) {
             soff[j] = (uint32_t)min(t0 + row - TW, a.M - 1) * (uint32_t)a.K + chunk * 16;
         }
     }
-    // scale slot q = 64 * wave + lane: As of token t0 + q, then Bs of weight
-    // block w0 / 128 + (q - TT) for the NBS blocks the tile spans; spare
-    // slots reload As[0, g] (never read)
-    const int q = 64 * wave + lane;
-    const float* sc_base;
-    int64_t sc_step;
-    if (q < TT) {
-        sc_base = a.As + (int64_t)min(t0 + q, a.M - 1) * a.as_sm;
-        sc_step = a.as_sk;
-    } else if (q < TT + NBS) {
-        sc_base = a.Bs + (int64_t)min(w0 / 128 + (q - TT), a.N / 128 - 1) * a.bs_sn;
-        sc_step = a.bs_sk;
-    } else {
-        sc_base = a.As;
-        sc_step = a.as_sk;
+    // scale slot q = 64 * (h * NWAVE + wave) + lane of slice h: As of token
+    // t0 + q, then Bs of weight block w0 / 128 + (q - TT) for the NBS blocks
+    // the tile spans, then bias dword (q - TT - NBS) = columns w0 + 2 (q - TT
+    // - NBS) and the next one (the same every group); spare slots, and the
+    // bias slots without a bias, reload As[0, g] (never read)
+    const float* sc_base[NSC];
+    int64_t sc_step[NSC];
+#pragma unroll
+    for (int h = 0; h < NSC; ++h) {
+        const int q = 64 * (h * NWAVE + wave) + lane;
+        if (q < TT) {
+            sc_base[h] = a.As + (int64_t)min(t0 + q, a.M - 1) * a.as_sm;
+            sc_step[h] = a.as_sk;
+        } else if (q < TT + NBS) {
+            sc_base[h] = a.Bs + (int64_t)min(w0 / 128 + (q - TT), a.N / 128 - 1) * a.bs_sn;
+            sc_step[h] = a.bs_sk;
+        } else if (q < TT + NBS + TW / 2 && a.bias) {
+            sc_base[h] = (const float*)(a.bias + min(w0 + 2 * (q - TT - NBS), a.N - 2));
+            sc_step[h] = 0;
+        } else {
+            sc_base[h] = a.As;
+            sc_step[h] = a.as_sk;
+        }
     }
     auto dma = [&](int g, int stage) {
         unsigned char* st = lds + stage * STAGE;
@@ -486,8 +510,10 @@ void fp8bg_ring(KArgs a) {
             __builtin_amdgcn_global_load_lds(
                 (const void*)(sbase[j] + (uint32_t)(soff[j] + (uint32_t)g * kGroupK)),
                 FP8BG_LDS_PTR(st + (wave * NJ + j) * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(sc_base + (int64_t)g * sc_step),
-                                         FP8BG_LDS_PTR(st + OPS + wave * 256), 4, 0, 0);
+#pragma unroll
+        for (int h = 0; h < NSC; ++h)
+            __builtin_amdgcn_global_load_lds((const void*)(sc_base[h] + (int64_t)g * sc_step[h]),
+                                             FP8BG_LDS_PTR(st + OPS + (h * NWAVE + wave) * 256), 4, 0, 0);
     };
 
     f32x4 acc[NW][NT];
@@ -576,20 +602,43 @@ void fp8bg_ring(KArgs a) {
     }
     __builtin_amdgcn_s_setprio(0);
     // The clamped loads of the last ST - 1 steps are still in flight: they
-    // must land before the workgroup's LDS can be handed to another one.
+    // must land before the LDS is reused below or handed to another workgroup.
     wait_vmcnt<0>();
 
-    // ---- epilogue (as fp8bg_tiled) ----
+    // ---- epilogue ----
     if (blockIdx.x < a.n_dp) {
+        // bf16 C through LDS: each wave writes 16 of its rows into its own
+        // slice (stage 0's operand area, free once every wave has passed the
+        // barrier below), reads them back as whole 16-byte chunks and stores
+        // full 128-byte lines with non-temporal stores (C is not re-read).
+        // Stored row-major with chunk c of row r at slot c ^ (r % CPR).
+        const uint16_t* bl = (const uint16_t*)(lds + ((kcount - 1) % ST) * STAGE + OPS +
+                                               (TT + NBS) * 4);
+        const int r = lane & 15, qd = lane >> 4;
+        uint2 bv[NW];
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+            bv[w] = *(const uint2*)(bl + wv_w * WTW + w * 16 + qd * 4);
+        wait_vmcnt_lds<0>();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        unsigned char* slice = lds + wave * (16 * ROWB);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const int m = t0 + wv_t * WTT + t * 16 + (lane & 15);
-            if (m >= a.M) continue;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                const int n = w0 + wv_w * WTW + w * 16 + (lane >> 4) * 4;
-                if (n >= a.N) continue;
-                *(uint2*)(a.C + (size_t)m * a.N + n) = out_bf16x4(acc[w][t], a.bias, n);
+            for (int w = 0; w < NW; ++w)
+                *(uint2*)(slice + r * ROWB + (((2 * w + (qd >> 1)) ^ (r % CPR)) << 4) + (qd & 1) * 8) =
+                    out_bf16x4v(acc[w][t], a.bias != nullptr, bv[w]);
+#pragma unroll
+            for (int h = 0; h < (16 * CPR + 63) / 64; ++h) {
+                const int idx = lane + 64 * h;
+                const int row = idx / CPR, c = idx % CPR;
+                if (row >= 16) continue;
+                const i32x4 v = *(const i32x4*)(slice + row * ROWB + ((c ^ (row % CPR)) << 4));
+                const int m = t0 + wv_t * WTT + t * 16 + row, n = w0 + wv_w * WTW + c * 8;
+                if (m < a.M && n < a.N)
+                    __builtin_nontemporal_store(v, (i32x4*)(a.C + (size_t)m * a.N + n));
             }
         }
         return;
@@ -987,7 +1036,9 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     if (skinny) {
         lds = (int64_t)k.wk * (k.tw / 16) * (k.tt / 16) * 64 * 16;
     } else if (ring) {
-        lds = (int64_t)k.stages * ((k.tw + k.tt) * 128 + k.ww * k.wt * 64 * 4);
+        const int nwave = k.ww * k.wt;
+        lds = (int64_t)k.stages * ((k.tw + k.tt) * 128 +
+                                   ring_scale_slices(k.tw, k.tt, nwave) * nwave * 64 * 4);
     } else {
         lds = 2LL * (k.tw + k.tt) * 128;
         if (cfg->flags & FP8BG_FLAG_SCALE_LDS) lds += (int64_t)k.tt * kg * 4;
