@@ -84,18 +84,23 @@ struct KArgs {
     int swz;               // LDS swizzle mode (see swz())
 };
 
-// fp32 -> bf16 bits, round to nearest even; any NaN -> 0x7fc0 (as torch).
-__device__ __forceinline__ uint32_t bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+// Two fp32 -> packed bf16 with gfx950's v_cvt_pk_bf16_f32: round to nearest
+// even, overflow to +-inf, subnormals kept (measured against an integer RNE
+// over every exponent class, all ties and subnormals).  Any NaN becomes
+// 0x7fc0 as in torch; it is made canonical first because the instruction
+// keeps a NaN's sign and payload.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    const f32x2 v = {__builtin_isnan(a) ? __builtin_nanf("") : a,
+                     __builtin_isnan(b) ? __builtin_nanf("") : b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 __device__ __forceinline__ uint2 pack_bf16x4(const f32x4& v) {
     uint2 o;
-    o.x = bf16_bits(v[0]) | (bf16_bits(v[1]) << 16);
-    o.y = bf16_bits(v[2]) | (bf16_bits(v[3]) << 16);
+    o.x = pack_bf16x2(v[0], v[1]);
+    o.y = pack_bf16x2(v[2], v[3]);
     return o;
 }
 
@@ -105,11 +110,12 @@ __device__ __forceinline__ uint2 pack_bf16x4(const f32x4& v) {
 // (out_bf16x4v: the same with the four bias values b already in registers.)
 __device__ __forceinline__ uint2 out_bf16x4v(const f32x4& v, bool has_bias, uint2 b) {
     if (!has_bias) return pack_bf16x4(v);
-    const uint32_t bb[4] = {b.x & 0xffffu, b.x >> 16, b.y & 0xffffu, b.y >> 16};
+    const uint2 c = pack_bf16x4(v);
+    const uint32_t cc[4] = {c.x << 16, c.x & 0xffff0000u, c.y << 16, c.y & 0xffff0000u};
+    const uint32_t bb[4] = {b.x << 16, b.x & 0xffff0000u, b.y << 16, b.y & 0xffff0000u};
     f32x4 r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        r[i] = __uint_as_float(bf16_bits(v[i]) << 16) + __uint_as_float(bb[i] << 16);
+    for (int i = 0; i < 4; ++i) r[i] = __uint_as_float(cc[i]) + __uint_as_float(bb[i]);
     return pack_bf16x4(r);
 }
 
@@ -433,7 +439,7 @@ void fp8bg_ring(KArgs a) {
     // epilogue: 16 output rows of a wave at a time, staged in LDS
     constexpr int ROWB = WTW * 2;                 // bf16 bytes of one wave row
     constexpr int CPR = ROWB / 16;                // 16-byte chunks per wave row
-    static_assert(NWAVE * 16 * ROWB <= OPS, "epilogue slices inside stage 0's operands");
+    static_assert(NWAVE * WTT * ROWB <= ST * STAGE, "epilogue regions inside the ring");
     static_assert(WTW <= 128 && 128 % WTW == 0, "wave weight rows inside one Bs block");
     static_assert(ST >= 2 && NDMA * (ST - 2) < 64, "ring depth");
     static_assert(ST * STAGE <= kMaxLds, "LDS");
@@ -503,17 +509,22 @@ void fp8bg_ring(KArgs a) {
             sc_step[h] = a.as_sk;
         }
     }
-    auto dma = [&](int g, int stage) {
-        unsigned char* st = lds + stage * STAGE;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-            __builtin_amdgcn_global_load_lds(
-                (const void*)(sbase[j] + (uint32_t)(soff[j] + (uint32_t)g * kGroupK)),
-                FP8BG_LDS_PTR(st + (wave * NJ + j) * 1024), 16, 0, 0);
+    auto dma_block = [&](int j, int g, int stage) {
+        __builtin_amdgcn_global_load_lds(
+            (const void*)(sbase[j] + (uint32_t)(soff[j] + (uint32_t)g * kGroupK)),
+            FP8BG_LDS_PTR(lds + stage * STAGE + (wave * NJ + j) * 1024), 16, 0, 0);
+    };
+    auto dma_scales = [&](int g, int stage) {
 #pragma unroll
         for (int h = 0; h < NSC; ++h)
-            __builtin_amdgcn_global_load_lds((const void*)(sc_base[h] + (int64_t)g * sc_step[h]),
-                                             FP8BG_LDS_PTR(st + OPS + (h * NWAVE + wave) * 256), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds(
+                (const void*)(sc_base[h] + (int64_t)g * sc_step[h]),
+                FP8BG_LDS_PTR(lds + stage * STAGE + OPS + (h * NWAVE + wave) * 256), 4, 0, 0);
+    };
+    auto dma = [&](int g, int stage) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) dma_block(j, g, stage);
+        dma_scales(g, stage);
     };
 
     f32x4 acc[NW][NT];
@@ -553,7 +564,13 @@ void fp8bg_ring(KArgs a) {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        dma(min(k_lo + i + ST - 1, g_last), (i + ST - 1) % ST);
+        // Loads of group i + ST - 1: the scale slices now, the operand blocks
+        // spread over the first half of the token-block loop below (block j
+        // before token block j * NT / (2 NJ)).  Issued together right after
+        // the barrier, the 8 waves' blocks queue at the address unit and hold
+        // back the first MFMAs; spread out, they overlap the MFMA stream.
+        const int g_next = min(k_lo + i + ST - 1, g_last), s_next = (i + ST - 1) % ST;
+        dma_scales(g_next, s_next);
         // Raised wave priority while this wave's MFMA stream is issued, so a
         // SIMD's two waves keep the matrix pipe fed ahead of memory issue.
         __builtin_amdgcn_s_setprio(1);
@@ -583,6 +600,9 @@ void fp8bg_ring(KArgs a) {
                 top_next = opread(st, TW + wv_t * WTT + (t + 1) * 16 + (lane & 15));
                 sa_next = sc[wv_t * WTT + (t + 1) * 16 + (lane & 15)];
             }
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+                if ((j * NT) / (2 * NJ) == t) dma_block(j, g_next, s_next);
             __builtin_amdgcn_sched_barrier(0);
             f32x4 cur[NW];
 #pragma unroll
@@ -607,11 +627,12 @@ void fp8bg_ring(KArgs a) {
 
     // ---- epilogue ----
     if (blockIdx.x < a.n_dp) {
-        // bf16 C through LDS: each wave writes 16 of its rows into its own
-        // slice (stage 0's operand area, free once every wave has passed the
-        // barrier below), reads them back as whole 16-byte chunks and stores
-        // full 128-byte lines with non-temporal stores (C is not re-read).
-        // Stored row-major with chunk c of row r at slot c ^ (r % CPR).
+        // bf16 C through LDS: once every wave has passed the barrier below the
+        // whole ring is free, and each wave writes its WTT x WTW tile into its
+        // own region (row-major, chunk c of row r at slot c ^ (r % CPR)),
+        // reads it back as whole 16-byte chunks and stores full 128-byte
+        // lines with non-temporal stores (C is not re-read).  The bias row
+        // sits in the last stage's scale area, so it is read first.
         const uint16_t* bl = (const uint16_t*)(lds + ((kcount - 1) % ST) * STAGE + OPS +
                                                (TT + NBS) * 4);
         const int r = lane & 15, qd = lane >> 4;
@@ -623,23 +644,24 @@ void fp8bg_ring(KArgs a) {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        unsigned char* slice = lds + wave * (16 * ROWB);
+        unsigned char* region = lds + wave * (WTT * ROWB);
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int w = 0; w < NW; ++w)
-                *(uint2*)(slice + r * ROWB + (((2 * w + (qd >> 1)) ^ (r % CPR)) << 4) + (qd & 1) * 8) =
+            for (int w = 0; w < NW; ++w) {
+                const int row = t * 16 + r;
+                *(uint2*)(region + row * ROWB + (((2 * w + (qd >> 1)) ^ (row % CPR)) << 4) + (qd & 1) * 8) =
                     out_bf16x4v(acc[w][t], a.bias != nullptr, bv[w]);
-#pragma unroll
-            for (int h = 0; h < (16 * CPR + 63) / 64; ++h) {
-                const int idx = lane + 64 * h;
-                const int row = idx / CPR, c = idx % CPR;
-                if (row >= 16) continue;
-                const i32x4 v = *(const i32x4*)(slice + row * ROWB + ((c ^ (row % CPR)) << 4));
-                const int m = t0 + wv_t * WTT + t * 16 + row, n = w0 + wv_w * WTW + c * 8;
-                if (m < a.M && n < a.N)
-                    __builtin_nontemporal_store(v, (i32x4*)(a.C + (size_t)m * a.N + n));
             }
+#pragma unroll
+        for (int h = 0; h < (WTT * CPR + 63) / 64; ++h) {
+            const int idx = lane + 64 * h;
+            const int row = idx / CPR, c = idx % CPR;
+            if (row >= WTT) continue;
+            const i32x4 v = *(const i32x4*)(region + row * ROWB + ((c ^ (row % CPR)) << 4));
+            const int m = t0 + wv_t * WTT + row, n = w0 + wv_w * WTW + c * 8;
+            if (m < a.M && n < a.N)
+                __builtin_nontemporal_store(v, (i32x4*)(a.C + (size_t)m * a.N + n));
         }
         return;
     }
