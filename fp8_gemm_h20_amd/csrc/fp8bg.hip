@@ -555,7 +555,6 @@ void fp8bg_ring(KArgs a) {
         // Stage i is complete once at most the DMA instructions of the ST - 2
         // later steps are outstanding (vmcnt retires in issue order); this
         // wave's LDS reads of stage (i - 1) % ST have all returned.
-        __builtin_amdgcn_s_setprio(0);
         wait_vmcnt_lds<NDMA * (ST - 2)>();
         // All waves' blocks of stage i have landed, and every wave is done
         // reading stage (i - 1) % ST, which is refilled next.  The empty asm
@@ -564,16 +563,12 @@ void fp8bg_ring(KArgs a) {
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        // Loads of group i + ST - 1: the scale slices now, the operand blocks
-        // spread over the first half of the token-block loop below (block j
-        // before token block j * NT / (2 NJ)).  Issued together right after
-        // the barrier, the 8 waves' blocks queue at the address unit and hold
-        // back the first MFMAs; spread out, they overlap the MFMA stream.
+        // Loads of group i + ST - 1, spread over the token-block loop below:
+        // operand block j before token block j * NT / (2 NJ), the scale
+        // slices before token block NT / 2.  Issued together right after the
+        // barrier, the waves' loads queue at the address unit and hold back
+        // the first MFMAs; spread out, they overlap the MFMA stream.
         const int g_next = min(k_lo + i + ST - 1, g_last), s_next = (i + ST - 1) % ST;
-        dma_scales(g_next, s_next);
-        // Raised wave priority while this wave's MFMA stream is issued, so a
-        // SIMD's two waves keep the matrix pipe fed ahead of memory issue.
-        __builtin_amdgcn_s_setprio(1);
 
         const unsigned char* st = lds + (i % ST) * STAGE;
         const float* sc = (const float*)(st + OPS);
@@ -603,6 +598,7 @@ void fp8bg_ring(KArgs a) {
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
                 if ((j * NT) / (2 * NJ) == t) dma_block(j, g_next, s_next);
+            if (t == NT / 2) dma_scales(g_next, s_next);
             __builtin_amdgcn_sched_barrier(0);
             f32x4 cur[NW];
 #pragma unroll
@@ -620,7 +616,6 @@ void fp8bg_ring(KArgs a) {
 #pragma unroll
         for (int w = 0; w < NW; ++w) promote(acc[w][NT - 1], prev[w], s_prev);
     }
-    __builtin_amdgcn_s_setprio(0);
     // The clamped loads of the last ST - 1 steps are still in flight: they
     // must land before the LDS is reused below or handed to another workgroup.
     wait_vmcnt<0>();
