@@ -11,7 +11,7 @@ from pathlib import Path
 
 LIB_NAME = "libfp8bg.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK = 0
 ERR_SHAPE = 1
@@ -42,6 +42,7 @@ EXPORTS = (
     "fp8bg_make_plan",
     "fp8bg_config_supported",
     "fp8bg_gemm",
+    "fp8bg_gemm_bf16a",
     "fp8bg_quant_act",
     "fp8bg_e4m3_encode_host",
     "fp8bg_strerror",
@@ -118,6 +119,17 @@ def _declare(lib):
         vp,                     # stream
     ]
     lib.fp8bg_gemm.restype = ctypes.c_int
+    lib.fp8bg_gemm_bf16a.argtypes = [
+        vp, i64, ctypes.c_float,  # X, row stride, eps
+        vp, vp, i64, i64,       # B, Bs, strides
+        vp,                     # bias (bf16 [N] or NULL)
+        vp, i32, i32, i32,      # C, M, N, K
+        ctypes.POINTER(Config), i32,
+        vp, i64,                # ws, ws_elems
+        vp, vp, i64, i64,       # q_out, s_out, s strides (or NULLs)
+        vp,                     # stream
+    ]
+    lib.fp8bg_gemm_bf16a.restype = ctypes.c_int
     lib.fp8bg_quant_act.argtypes = [vp, i64, vp, vp, i64, i64, i32, i32, ctypes.c_float, vp]
     lib.fp8bg_quant_act.restype = ctypes.c_int
     lib.fp8bg_e4m3_encode_host.argtypes = [vp, vp, i64]

@@ -82,6 +82,13 @@ struct KArgs {
     int xcd_remap;
     int scale_lds;
     int swz;               // LDS swizzle mode (see swz())
+    // bf16 activations quantised inside the skinny kernel (fp8bg_gemm_bf16a)
+    const uint16_t* X;     // [M, K] bf16, row stride ldx elements
+    int64_t ldx;
+    float eps;
+    uint8_t* q_out;        // optional [M, K] e4m3 copy of the quantised activations
+    float* s_out;          // optional [M, K/128] scales, strides qs_sm, qs_sk
+    int64_t qs_sm, qs_sk;
 };
 
 // Two fp32 -> packed bf16 with gfx950's v_cvt_pk_bf16_f32: round to nearest
@@ -675,7 +682,15 @@ void fp8bg_ring(KArgs a) {
 // ===========================================================================
 // Small-M kernel: operands straight from global memory, waves split K
 // ===========================================================================
-template <int NWB, int NTB, int S, int U>
+// With QA the token operand is quantised in registers from bf16 activations:
+// the four lanes holding one token's 128-K group reduce its amax by lane
+// shuffles, s = max(amax, eps) / 448 and each value becomes
+// e4m3(x * (1 / s)) through v_cvt_pk_fp8_f32 (round to nearest even; the
+// same code as the integer encoder for every non-NaN input).  The
+// reciprocal replaces the standalone quantiser's division: one multiply per
+// value instead of a division sequence, which is what makes the fused path
+// cheaper than a separate kernel.
+template <int NWB, int NTB, int S, int U, int QA>
 __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     constexpr int TW = 16 * NWB, TT = 16 * NTB, NB = NWB * NTB;
     __shared__ f32x4 red[S][NB][64];
@@ -713,12 +728,19 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     }
     const uint8_t* tp[NTB];
     const float* asp[NTB];
+    const uint16_t* xp[NTB];
 #pragma unroll
     for (int t = 0; t < NTB; ++t) {
         const int m = min(t0 + 16 * t + r, a.M - 1);
-        tp[t] = a.A + (size_t)m * a.K + 32 * q;
-        asp[t] = a.As + (int64_t)m * a.as_sm;
+        if (QA) {
+            xp[t] = a.X + (size_t)m * a.ldx + 32 * q;
+        } else {
+            tp[t] = a.A + (size_t)m * a.K + 32 * q;
+            asp[t] = a.As + (int64_t)m * a.as_sm;
+        }
     }
+    // side outputs of the fused quantiser come from the first weight tile
+    const bool qa_write = QA && a.q_out != nullptr && pw == 0;
 
     f32x4 acc[NWB][NTB];
 #pragma unroll
@@ -730,6 +752,7 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     const int J = wave < kcount ? (kcount - 1 - wave) / S + 1 : 0;
     for (int j0 = 0; j0 < J; j0 += U) {
         i32x8 wv[U][NWB], tv[U][NTB];
+        i32x4 xr[QA ? U : 1][QA ? NTB : 1][4];
         float sa[U][NTB], sb[U][NWB];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -742,8 +765,64 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                 }
 #pragma unroll
                 for (int t = 0; t < NTB; ++t) {
-                    tv[u][t] = load_op(tp[t] + (size_t)g * kGroupK);
-                    sa[u][t] = asp[t][(int64_t)g * a.as_sk];
+                    if (QA) {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            xr[u][t][c] = *(const i32x4*)(xp[t] + (size_t)g * kGroupK + 8 * c);
+                    } else {
+                        tv[u][t] = load_op(tp[t] + (size_t)g * kGroupK);
+                        sa[u][t] = asp[t][(int64_t)g * a.as_sk];
+                    }
+                }
+            }
+        }
+        if (QA) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (j0 + u < J) {
+                    const int g = k_lo + wave + S * (j0 + u);
+#pragma unroll
+                    for (int t = 0; t < NTB; ++t) {
+                        float v[32];
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                v[8 * c + 2 * i] = __uint_as_float((uint32_t)xr[u][t][c][i] << 16);
+                                v[8 * c + 2 * i + 1] = __uint_as_float((uint32_t)xr[u][t][c][i] & 0xffff0000u);
+                            }
+                        float amax = 0.f;
+                        bool nan = false;
+#pragma unroll
+                        for (int i = 0; i < 32; ++i) {
+                            amax = fmaxf(amax, fabsf(v[i]));
+                            nan |= __builtin_isnan(v[i]);
+                        }
+                        // lanes r, r + 16, r + 32, r + 48 hold the token's group
+#pragma unroll
+                        for (int d = 16; d < 64; d <<= 1) {
+                            amax = fmaxf(amax, __shfl_xor(amax, d));
+                            nan |= __shfl_xor((int)nan, d) != 0;
+                        }
+                        const float sc = nan ? __builtin_nanf("") : fmaxf(amax, a.eps) / 448.0f;
+                        const float rcp = 1.0f / sc;
+                        i32x8 o;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            int d = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * i] * rcp, v[4 * i + 1] * rcp, 0, false);
+                            d = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * i + 2] * rcp, v[4 * i + 3] * rcp, d, true);
+                            o[i] = d;
+                        }
+                        tv[u][t] = o;
+                        sa[u][t] = sc;
+                        const int m = t0 + 16 * t + r;
+                        if (qa_write && m < a.M) {
+                            uint8_t* qd = a.q_out + (size_t)m * a.K + (size_t)g * kGroupK + 32 * q;
+                            *(i32x4*)qd = (i32x4){o[0], o[1], o[2], o[3]};
+                            *(i32x4*)(qd + 16) = (i32x4){o[4], o[5], o[6], o[7]};
+                            if (q == 0) a.s_out[m * a.qs_sm + g * a.qs_sk] = sc;
+                        }
+                    }
                 }
             }
         }
@@ -922,6 +1001,13 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(256, 128, 4, 2, 3, 0) X(256, 128, 4, 2, 2, 0) X(128, 256, 2, 4, 2, 0)    \
     X(256, 128, 4, 1, 2, 2) X(128, 128, 2, 2, 2, 2)
 
+// skinny with the fused activation quantiser: the 16-token (NT = 1) tiles
+// (4, 1, 8, 4) left out: with the bf16 staging it needs more than 256 VGPRs
+#define FP8BG_SKINNY_QA(X)                                                     \
+    X(1, 1, 4, 1) X(1, 1, 4, 2) X(1, 1, 8, 1) X(1, 1, 8, 2) X(1, 1, 8, 4)      \
+    X(2, 1, 4, 1) X(2, 1, 4, 2) X(2, 1, 8, 1) X(2, 1, 8, 2) X(2, 1, 8, 4)      \
+    X(4, 1, 4, 1) X(4, 1, 4, 2) X(4, 1, 8, 1) X(4, 1, 8, 2)
+
 struct Instance {
     int kind, tw, tt, ww, wt, wk, unroll, stages, kf, threads;
     void (*launch)(dim3 grid, size_t shm, hipStream_t s, const KArgs& a);
@@ -938,10 +1024,18 @@ FP8BG_TILED(FP8BG_TILED_LAUNCHER)
 #define FP8BG_SKINNY_LAUNCHER(NW, NT, S, U)                                                  \
     static void skinny_##NW##_##NT##_##S##_##U(dim3 g, size_t shm, hipStream_t s,           \
                                                const KArgs& a) {                            \
-        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U>), g, dim3(64 * S), shm, s, a);        \
+        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, 0>), g, dim3(64 * S), shm, s, a);     \
     }
 FP8BG_SKINNY(FP8BG_SKINNY_LAUNCHER)
 #undef FP8BG_SKINNY_LAUNCHER
+
+#define FP8BG_SKINNY_QA_LAUNCHER(NW, NT, S, U)                                               \
+    static void skinny_qa_##NW##_##NT##_##S##_##U(dim3 g, size_t shm, hipStream_t s,        \
+                                                  const KArgs& a) {                         \
+        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, 1>), g, dim3(64 * S), shm, s, a);     \
+    }
+FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_LAUNCHER)
+#undef FP8BG_SKINNY_QA_LAUNCHER
 
 #define FP8BG_RING_LAUNCHER(TW, TT, WW, WT, ST, KF)                                          \
     static void ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF(dim3 g, size_t shm,            \
@@ -961,10 +1055,25 @@ FP8BG_RING(FP8BG_RING_LAUNCHER)
      ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF},
 const Instance kInstances[] = {FP8BG_TILED(FP8BG_TILED_ENTRY) FP8BG_SKINNY(FP8BG_SKINNY_ENTRY)
                                    FP8BG_RING(FP8BG_RING_ENTRY)};
+#define FP8BG_SKINNY_QA_ENTRY(NW, NT, S, U) \
+    {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 1, 0, 64 * S, skinny_qa_##NW##_##NT##_##S##_##U},
+const Instance kQaInstances[] = {FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_ENTRY)};
 #undef FP8BG_TILED_ENTRY
 #undef FP8BG_SKINNY_ENTRY
+#undef FP8BG_SKINNY_QA_ENTRY
 #undef FP8BG_RING_ENTRY
 constexpr int kNumInstances = sizeof(kInstances) / sizeof(kInstances[0]);
+constexpr int kNumQaInstances = sizeof(kQaInstances) / sizeof(kQaInstances[0]);
+
+int find_qa_instance(const fp8bg_config* c) {
+    for (int i = 0; i < kNumQaInstances; ++i) {
+        const Instance& k = kQaInstances[i];
+        if (c->kind == FP8BG_KIND_SKINNY && k.tw == c->block_w && k.tt == c->block_t &&
+            k.wk == c->waves_k && k.unroll == c->unroll && c->k_fixed == 0)
+            return i;
+    }
+    return -1;
+}
 
 int find_instance(const fp8bg_config* c) {
     for (int i = 0; i < kNumInstances; ++i) {
@@ -1092,7 +1201,7 @@ int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_
         return FP8BG_ERR_WORKSPACE;
 
     const Instance& k = kInstances[p.kernel_id];
-    KArgs a;
+    KArgs a = {};
     a.A = (const uint8_t*)A;
     a.B = (const uint8_t*)B;
     a.As = As;
@@ -1124,6 +1233,64 @@ int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_
     if (p.n_split > 0) {
         hipLaunchKernelGGL(fp8bg_split_reduce, dim3(p.n_split), dim3(kThreads), 0, s, a,
                            k.kind == FP8BG_KIND_SKINNY ? 1 : 0);
+        if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
+    }
+    return FP8BG_OK;
+}
+
+int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps, const void* B, const float* Bs,
+                     int64_t bs_stride_n, int64_t bs_stride_k, const void* bias, void* C, int32_t M,
+                     int32_t N, int32_t K, const fp8bg_config* cfg, int32_t num_cus, float* ws,
+                     int64_t ws_elems, void* q_out, float* s_out, int64_t s_stride_m,
+                     int64_t s_stride_k, void* stream) {
+    if (!X || !B || !Bs || !C || !cfg) return FP8BG_ERR_NULL;
+    if ((q_out == nullptr) != (s_out == nullptr)) return FP8BG_ERR_NULL;
+    const int qi = find_qa_instance(cfg);
+    if (qi < 0) return FP8BG_ERR_CONFIG;
+    // 1 / (max(amax, eps) / 448) stays finite
+    if (!(eps >= 1e-30f) || !(eps < 3.4e38f)) return FP8BG_ERR_CONFIG;
+    fp8bg_plan p;
+    const int rc = fp8bg_make_plan(M, N, K, cfg, num_cus, &p);
+    if (rc != FP8BG_OK) return rc;
+    if (x_stride_m < K) return FP8BG_ERR_SHAPE;
+    if ((((uintptr_t)X) | ((uintptr_t)B) | ((uintptr_t)C) | ((uintptr_t)q_out)) & 15 ||
+        (x_stride_m % 8) || (((uintptr_t)bias) & 7) || (((uintptr_t)s_out) & 3))
+        return FP8BG_ERR_ALIGN;
+    if (p.n_split > 0 && (!ws || ws_elems < p.ws_elems || (((uintptr_t)ws) & 15)))
+        return FP8BG_ERR_WORKSPACE;
+
+    const Instance& k = kQaInstances[qi];
+    KArgs a = {};
+    a.B = (const uint8_t*)B;
+    a.Bs = Bs;
+    a.C = (uint16_t*)C;
+    a.bias = (const uint16_t*)bias;
+    a.ws = ws;
+    a.bs_sn = bs_stride_n;
+    a.bs_sk = bs_stride_k;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.tw = k.tw;
+    a.tt = k.tt;
+    a.tiles_w = p.tiles_w;
+    a.tiles_t = p.tiles_t;
+    a.n_dp = p.n_dp;
+    a.split = p.split;
+    a.group_t = cfg->group_t;
+    a.xcd_remap = (cfg->flags & FP8BG_FLAG_XCD_REMAP) ? 1 : 0;
+    a.X = (const uint16_t*)X;
+    a.ldx = x_stride_m;
+    a.eps = eps;
+    a.q_out = (uint8_t*)q_out;
+    a.s_out = s_out;
+    a.qs_sm = s_stride_m;
+    a.qs_sk = s_stride_k;
+    hipStream_t s = (hipStream_t)stream;
+    k.launch(dim3(p.grid), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
+    if (p.n_split > 0) {
+        hipLaunchKernelGGL(fp8bg_split_reduce, dim3(p.n_split), dim3(kThreads), 0, s, a, 1);
         if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
     }
     return FP8BG_OK;

@@ -74,18 +74,67 @@ def quantize_act(x, *, eps=1e-10, column_major_scales=False):
         return kernels.quant_act(x2, m, k, eps, column_major_scales)
 
 
-def linear(x, B, Bs, *, profile="35b_tp1", bias=None, eps=1e-10):
+def linear(x, B, Bs, *, profile="35b_tp1", bias=None, eps=1e-10, fused=None):
     """y = x @ dequant(B, Bs)^T (+ bias) for bf16 activations x[..., K].
 
     The dense block-FP8 linear of the reference's SGLang adapter
     (fp8mm_w8a8_block_fp8_linear, sgl_patch/fp8mm_sglang_patch.py:34-57):
     per-token-group quantisation of x, matmul with the bias added in the
     kernel epilogue (bit-identical to the adapter's `out + bias`), and the
-    result viewed as x.shape[:-1] + (N,).  Two kernels, no host sync.  Shapes
-    the profile does not cover raise ValueError (the adapter's own fallback
-    decision stays with the caller, as `supports` answers it).
+    result viewed as x.shape[:-1] + (N,).  No host sync.  Shapes the profile
+    does not cover raise ValueError (the adapter's own fallback decision
+    stays with the caller, as `supports` answers it).
+
+    Where the profile's entry for (M, N, K) is a 16-token skinny
+    configuration (decode sizes), the quantiser runs inside the GEMM kernel
+    (one launch instead of two, fp8bg_gemm_bf16a); its codes are
+    e4m3(x * (1/s)) rather than e4m3(x / s), equal except on rare rounding
+    ties of the two quotients.  fused=False forces the two-kernel path,
+    fused=True requires the fused one (ValueError if the entry does not
+    allow it).
     """
+    import torch
+    from . import kernels
     n, k = B.shape
+    if fused is not False and x.dtype == torch.bfloat16 and x.is_cuda and x.shape[-1] == k \
+            and x.numel() > 0:
+        m = x.numel() // k
+        entry, _ = _select(profile, m, n, k)
+        ok = kernels.fused_config_ok(entry) and eps >= 1e-30
+        if fused and not ok:
+            raise ValueError("the profile entry for this shape is not a 16-token skinny "
+                             "configuration; the fused linear does not apply")
+        if ok:
+            _check_weights(B, Bs, x.device, bias)
+            x2 = x.reshape(-1, k)
+            if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+                x2 = x2.clone(memory_format=torch.contiguous_format)
+            with torch.cuda.device(x.device):
+                out = kernels.linear_fused(x2, B, Bs, dict(entry["config"]), eps, bias=bias)
+            return out.view(*x.shape[:-1], n)
+    elif fused:
+        raise ValueError("fused linear needs bf16 CUDA activations with last dim K")
     q, s = quantize_act(x, eps=eps)
     out = matmul(q, B, s, Bs, profile=profile, bias=bias)
     return out.view(*x.shape[:-1], n)
+
+
+def _check_weights(B, Bs, device, bias):
+    """Weight-side checks of matmul (dispatch.py:12-27 order) for the fused linear."""
+    import torch
+    n, k = B.shape
+    if k % 128 or n % 128:
+        raise ValueError("A/B dimensions must match and N,K must be multiples of 128")
+    if B.dtype != torch.float8_e4m3fn:
+        raise ValueError("A and B must be float8_e4m3fn")
+    if B.device != device or Bs.device != device:
+        raise ValueError("All tensors must reside on the same CUDA device")
+    if not B.is_contiguous():
+        raise ValueError("A and B must be contiguous row-major tensors")
+    if Bs.dtype != torch.float32:
+        raise ValueError("Scales must be float32")
+    if tuple(Bs.shape) != (n // 128, k // 128):
+        raise ValueError("Expected As[M,K/128] and Bs[N/128,K/128]")
+    if bias is not None and (bias.dtype != torch.bfloat16 or tuple(bias.shape) != (n,)
+                             or bias.device != device or not bias.is_contiguous()):
+        raise ValueError("bias must be a contiguous bfloat16 [N] tensor on A's device")

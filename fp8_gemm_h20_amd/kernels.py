@@ -56,6 +56,9 @@ SKINNY = (
 )
 # skinny instances as (block_w, block_t, waves_k, unroll)
 SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
+# skinny with the activation quantiser fused (16-token tiles, except the one
+# that would spill); must match FP8BG_SKINNY_QA in csrc/fp8bg.hip
+SKINNY_QA = tuple(c for c in SKINNY if c[1] == 1 and c != (4, 1, 8, 4))
 # ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed)
 RING = (
     (256, 128, 4, 1, 3, 0), (256, 128, 2, 2, 3, 0), (128, 128, 2, 2, 4, 0),
@@ -256,6 +259,47 @@ def quant_act(x2, m, k, eps, column_major_scales):
     _lib.check(_lib.lib().fp8bg_quant_act(x2.data_ptr(), x2.stride(0), q.data_ptr(), s.data_ptr(),
                                           s.stride(0), s.stride(1), m, k, ctypes.c_float(eps), stream))
     return q, s
+
+
+def linear_fused(x2, B, Bs, config, eps, bias=None, out=None, keep_quantized=False):
+    """Decode-size linear in one launch: the skinny kernel with the activation
+    quantiser fused (C ABI fp8bg_gemm_bf16a).  `x2` is a [M, K] bf16 view with
+    unit column stride; `config` a skinny table entry with BLOCK_T == 16.
+    Returns C, or (C, q, s) with the codes and scales the kernel used when
+    keep_quantized is set."""
+    import torch
+    m, k = x2.shape
+    n = B.shape[0]
+    dev = x2.device
+    cstruct = _skinny_cached(_freeze(config))
+    cus = num_cus(dev)
+    plan = _lib.make_plan(m, n, k, cstruct, cus)
+    C = torch.empty((m, n), device=dev, dtype=torch.bfloat16) if out is None else out
+    ws_ptr, ws_n = None, 0
+    if plan.n_split:
+        ws = _workspace(dev, plan.ws_elems)
+        ws_ptr, ws_n = ws.data_ptr(), ws.numel()
+    q = s = None
+    if keep_quantized:
+        q = torch.empty((m, k), device=dev, dtype=torch.float8_e4m3fn)
+        s = torch.empty((m, k // 128), device=dev, dtype=torch.float32)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    _lib.check(_lib.lib().fp8bg_gemm_bf16a(
+        x2.data_ptr(), x2.stride(0), ctypes.c_float(eps),
+        B.data_ptr(), Bs.data_ptr(), Bs.stride(0), Bs.stride(1),
+        None if bias is None else bias.data_ptr(),
+        C.data_ptr(), m, n, k, ctypes.byref(cstruct), cus, ws_ptr, ws_n,
+        None if q is None else q.data_ptr(), None if s is None else s.data_ptr(),
+        0 if s is None else s.stride(0), 0 if s is None else s.stride(1), stream))
+    return (C, q, s) if keep_quantized else C
+
+
+def fused_config_ok(entry):
+    """True when a table entry can run as the fused-quantiser skinny kernel."""
+    c = entry["config"]
+    return (entry["impl"] == "skinny" and int(c.get("BLOCK_T", 0)) == 16
+            and (int(c["BLOCK_W"]) // 16, 1, int(c.get("WAVES_K", 8)), int(c.get("UNROLL", 1)))
+            in SKINNY_QA)
 
 
 def _freeze(config):

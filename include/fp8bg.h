@@ -40,7 +40,7 @@ extern "C" {
 
 /* ABI version returned by fp8bg_version(); bumped on any signature or struct
  * change. */
-#define FP8BG_ABI_VERSION 3
+#define FP8BG_ABI_VERSION 4
 
 /* ---- kernel kinds --------------------------------------------------------- */
 /* LDS-tiled kernel: a block_w x block_t workgroup tile, 4 waves in a
@@ -192,6 +192,32 @@ int fp8bg_gemm(const void* A, const void* B,
 int fp8bg_quant_act(const void* x, int64_t x_stride_m, void* q,
                     float* s, int64_t s_stride_m, int64_t s_stride_k,
                     int32_t M, int32_t K, float eps, void* stream);
+
+/*
+ * The dense block-FP8 linear for small M in one kernel: bf16 activations
+ * X[M,K] (row stride x_stride_m elements, 16-byte rows) are quantised per
+ * 1x128 group inside the skinny GEMM kernel and multiplied with B/Bs as
+ * fp8bg_gemm does, adding the optional bias.  Replaces the adapter's pair
+ * per_token_group_quant_fp8 + matmul (sgl_patch/fp8mm_sglang_patch.py:51-54)
+ * for decode-size M.
+ *   - cfg must be a compiled skinny configuration with block_t == 16
+ *     (else FP8BG_ERR_CONFIG); any M >= 1 is accepted.
+ *   - Scales: s = max(amax, eps) / 448 exactly as fp8bg_quant_act, codes
+ *     e4m3(x * (1/s)) with round to nearest even.  The reciprocal differs
+ *     from fp8bg_quant_act's x / s by at most one e4m3 step on rare values,
+ *     so results agree with quantise-then-gemm to the GEMM tolerance, not
+ *     bitwise.  eps must be >= 1e-30.
+ *   - q_out/s_out (both or neither) receive the codes and scales it used
+ *     (s strides in elements); q_out 16-byte aligned.
+ *   - ws as for fp8bg_gemm when the configuration splits K.
+ */
+int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps,
+                     const void* B, const float* Bs, int64_t bs_stride_n,
+                     int64_t bs_stride_k, const void* bias, void* C,
+                     int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg,
+                     int32_t num_cus, float* ws, int64_t ws_elems,
+                     void* q_out, float* s_out, int64_t s_stride_m,
+                     int64_t s_stride_k, void* stream);
 
 /*
  * Host copy of the kernels' fp32 -> e4m3 conversion (round to nearest even,

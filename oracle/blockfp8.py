@@ -136,6 +136,21 @@ def quantize_act(x, eps=1e-6):
     return q, s
 
 
+def quantize_act_reciprocal(x, eps=1e-10):
+    """The fused-quantiser GEMM's activation recipe (fp8bg_gemm_bf16a):
+    scales as quantize_act, codes e4m3(x * (1/s)) with 1/s and the product
+    rounded to fp32.  It differs from quantize_act's x / s only where the two
+    fp32 values straddle an e4m3 rounding boundary."""
+    x = np.asarray(x, dtype=np.float32)
+    m, k = x.shape
+    xg = x.reshape(m, k // GROUP, GROUP)
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        s = (np.maximum(np.abs(xg).max(-1), np.float32(eps)) / np.float32(E4M3_MAX)).astype(np.float32)
+        r = (np.float32(1) / s).astype(np.float32)
+        q = e4m3_encode((xg * r[:, :, None]).astype(np.float32)).reshape(m, k)
+    return q, s
+
+
 def quantize_weight(w, eps=1e-6):
     """w[N,K] fp32 -> (e4m3 codes [N,K], Bs[N/128,K/128]) per 128x128 block."""
     w = np.asarray(w, dtype=np.float32)

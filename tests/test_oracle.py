@@ -229,3 +229,29 @@ def test_config0_fixture_reproduces(golden_dir):
     assert abs(np.abs(C).max() - cfg["c_absmax"]) <= 1e-5 * cfg["c_absmax"]
     for i, j, v in cfg["samples"]:
         assert abs(C[i, j] - v) <= 1e-5 * cfg["c_absmax"]
+
+
+def test_reciprocal_quantiser_differs_from_division_only_at_rounding_boundaries():
+    # The fused GEMM's recipe e4m3(x * (1/s)) against quantize_act's e4m3(x / s):
+    # identical scales; codes equal except where the two fp32 quotients fall on
+    # opposite sides of an e4m3 rounding boundary, and then one step apart.
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((64, 4096)) * 3).astype(np.float32)
+    q1, s1 = ob.quantize_act(x, eps=1e-10)
+    q2, s2 = ob.quantize_act_reciprocal(x, eps=1e-10)
+    assert np.array_equal(s1, s2)
+    d = q1 != q2
+    assert d.mean() < 2e-3
+    v1 = ob.e4m3_decode(q1[d]).astype(np.float64)
+    v2 = ob.e4m3_decode(q2[d]).astype(np.float64)
+    codes = np.sort(ob.e4m3_decode(np.arange(256, dtype=np.uint8))[~np.isnan(ob.e4m3_decode(np.arange(256, dtype=np.uint8)))])
+    i1 = np.searchsorted(codes, v1)
+    i2 = np.searchsorted(codes, v2)
+    assert np.all(np.abs(i1 - i2) == 1)
+    # a power-of-two scale makes both quotients exact: every code comes back
+    vals = ob.e4m3_decode(np.arange(0, 127, dtype=np.uint8)).astype(np.float32)   # 0 .. 448
+    row = np.concatenate([vals, -vals[1:2]]) * np.float32(2.0 ** -3)             # amax 56: s = 1/8
+    q1, s1 = ob.quantize_act(row[None, :], eps=1e-10)
+    q2, s2 = ob.quantize_act_reciprocal(row[None, :], eps=1e-10)
+    assert s1[0, 0] == s2[0, 0] == np.float32(0.125)
+    assert np.array_equal(q1, q2) and np.array_equal(q1[0, :127], np.arange(0, 127, dtype=np.uint8))
