@@ -869,8 +869,11 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
 // ===========================================================================
 // Split-K reduction: one workgroup per split tile, fixed split order.
 // ===========================================================================
-__global__ __launch_bounds__(kThreads) void fp8bg_split_reduce(KArgs a, int skinny_order) {
-    const int stile = blockIdx.x;
+// `parts` workgroups share one split tile, each taking every parts-th run of
+// kThreads * 4 elements, so a small tail of split tiles still spreads over
+// the whole GPU.
+__global__ __launch_bounds__(kThreads) void fp8bg_split_reduce(KArgs a, int skinny_order, int parts) {
+    const int stile = blockIdx.x / parts, part = blockIdx.x % parts;
     int w0, t0;
     if (skinny_order) {
         w0 = (stile / a.tiles_t) * a.tw;
@@ -880,7 +883,7 @@ __global__ __launch_bounds__(kThreads) void fp8bg_split_reduce(KArgs a, int skin
     }
     const int tile_el = a.tw * a.tt;
     const float* base = a.ws + (size_t)stile * a.split * tile_el;
-    for (int e = threadIdx.x * 4; e < tile_el; e += kThreads * 4) {
+    for (int e = (part * kThreads + threadIdx.x) * 4; e < tile_el; e += parts * kThreads * 4) {
         const int tl = e / a.tw, wl = e % a.tw;
         const int m = t0 + tl, n = w0 + wl;
         if (m >= a.M || n >= a.N) continue;
@@ -1065,6 +1068,14 @@ const Instance kQaInstances[] = {FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_ENTRY)};
 constexpr int kNumInstances = sizeof(kInstances) / sizeof(kInstances[0]);
 constexpr int kNumQaInstances = sizeof(kQaInstances) / sizeof(kQaInstances[0]);
 
+// Workgroups per split tile in the reduction: enough for about two per CU,
+// at most one per kThreads * 4 elements of the tile.
+int reduce_parts(const fp8bg_plan& p, const Instance& k, int num_cus) {
+    const int max_parts = max(1, k.tw * k.tt / (kThreads * 4));
+    const int want = (2 * num_cus + p.n_split - 1) / p.n_split;
+    return max(1, min(want, max_parts));
+}
+
 int find_qa_instance(const fp8bg_config* c) {
     for (int i = 0; i < kNumQaInstances; ++i) {
         const Instance& k = kQaInstances[i];
@@ -1231,8 +1242,9 @@ int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_
     k.launch(dim3(p.grid), shm, s, a);
     if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
     if (p.n_split > 0) {
-        hipLaunchKernelGGL(fp8bg_split_reduce, dim3(p.n_split), dim3(kThreads), 0, s, a,
-                           k.kind == FP8BG_KIND_SKINNY ? 1 : 0);
+        const int parts = reduce_parts(p, k, num_cus);
+        hipLaunchKernelGGL(fp8bg_split_reduce, dim3(p.n_split * parts), dim3(kThreads), 0, s, a,
+                           k.kind == FP8BG_KIND_SKINNY ? 1 : 0, parts);
         if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
     }
     return FP8BG_OK;
@@ -1290,7 +1302,9 @@ int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps, const void* B
     k.launch(dim3(p.grid), 0, s, a);
     if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
     if (p.n_split > 0) {
-        hipLaunchKernelGGL(fp8bg_split_reduce, dim3(p.n_split), dim3(kThreads), 0, s, a, 1);
+        const int parts = reduce_parts(p, k, num_cus);
+        hipLaunchKernelGGL(fp8bg_split_reduce, dim3(p.n_split * parts), dim3(kThreads), 0, s, a, 1,
+                           parts);
         if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
     }
     return FP8BG_OK;
