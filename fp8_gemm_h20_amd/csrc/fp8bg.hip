@@ -31,12 +31,16 @@
 //                   and the S waves of a workgroup split the K groups of one
 //                   tile among themselves (deep memory-level parallelism for
 //                   weight streaming); the S partial tiles are summed through
-//                   LDS in fixed wave order.
+//                   LDS in fixed wave order.  The QA variant reads bf16
+//                   activations and quantises them in registers (the fused
+//                   decode linear, fp8bg_gemm_bf16a).
 //  * fp8bg_ring   - large-tile kernel: direct global->LDS loads
 //                   (global_load_lds_dwordx4) into an ST-stage LDS ring, one
-//                   barrier per 128-K group, 4 or 8 waves; same epilogue and
-//                   split-K handling as fp8bg_tiled.
+//                   barrier per 128-K group, 4 or 8 waves, the next group's
+//                   loads spread over the MFMA stream; C staged through LDS
+//                   and written as whole lines; split-K as fp8bg_tiled.
 //  * fp8bg_split_reduce - fixed-order sum of split-K partials -> bf16.
+//  * fp8bg_quant_act_kernel - bf16 activations -> e4m3 + fp32 group scales.
 // Every reduction order is fixed by the configuration, so results are bitwise
 // reproducible run to run and under hipGraph replay.  No kernel uses atomics,
 // fences beyond workgroup scope, or spin waits.
@@ -1002,7 +1006,8 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(128, 64, 4, 1, 4, 0) X(128, 64, 2, 2, 3, 0) X(64, 64, 4, 1, 4, 0)        \
     X(256, 64, 4, 1, 3, 0) X(128, 32, 4, 1, 4, 0) X(256, 256, 4, 2, 2, 0)      \
     X(256, 128, 4, 2, 3, 0) X(256, 128, 4, 2, 2, 0) X(128, 256, 2, 4, 2, 0)    \
-    X(256, 128, 4, 1, 2, 2) X(128, 128, 2, 2, 2, 2)
+    X(256, 128, 4, 1, 2, 2) X(128, 128, 2, 2, 2, 2)                            \
+    X(64, 64, 4, 1, 8, 0) X(128, 64, 4, 1, 6, 0) X(128, 32, 4, 1, 7, 0)
 
 // skinny with the fused activation quantiser: the 16-token (NT = 1) tiles
 // (4, 1, 8, 4) left out: with the bf16 staging it needs more than 256 VGPRs
