@@ -1007,7 +1007,8 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(256, 64, 4, 1, 3, 0) X(128, 32, 4, 1, 4, 0) X(256, 256, 4, 2, 2, 0)      \
     X(256, 128, 4, 2, 3, 0) X(256, 128, 4, 2, 2, 0) X(128, 256, 2, 4, 2, 0)    \
     X(256, 128, 4, 1, 2, 2) X(128, 128, 2, 2, 2, 2)                            \
-    X(64, 64, 4, 1, 8, 0) X(128, 64, 4, 1, 6, 0) X(128, 32, 4, 1, 7, 0)
+    X(64, 64, 4, 1, 8, 0) X(128, 64, 4, 1, 6, 0) X(128, 32, 4, 1, 7, 0)        \
+    X(128, 128, 2, 2, 2, 0)
 
 // skinny with the fused activation quantiser: the 16-token (NT = 1) tiles
 // (4, 1, 8, 4) left out: with the bf16 staging it needs more than 256 VGPRs

@@ -68,6 +68,7 @@ RING = (
     (256, 128, 4, 2, 3, 0), (256, 128, 4, 2, 2, 0), (128, 256, 2, 4, 2, 0),
     (256, 128, 4, 1, 2, 2), (128, 128, 2, 2, 2, 2),
     (64, 64, 4, 1, 8, 0), (128, 64, 4, 1, 6, 0), (128, 32, 4, 1, 7, 0),
+    (128, 128, 2, 2, 2, 0),
 )
 # back-compat name used by tests and the tuner
 INSTANCES = TILED
