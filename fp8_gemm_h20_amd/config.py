@@ -58,6 +58,7 @@ def _native_ok(impl, c, k):
     if c.get("LDS_SWIZZLE", "row16") not in ("row8", "row16", "pair"):
         return False
     if impl == "ring":
+        c = {key: v for key, v in c.items() if key not in ("M_SPLIT", "TAIL")}
         kf = c.get("K_FIXED", 0)
         return (c.get("SPLIT_MODE", "none") in _SPLIT_MODES and (kf == 0 or k == 256 * kf // 2) and
                 (tw, tt, c.get("WAVES_W"), c.get("WAVES_T"), c.get("STAGES"), kf) in RING)
@@ -87,6 +88,15 @@ def _check_entry(field, nk, k, m, entry, policy):
         raise ValueError(f"Invalid tile: {where}")
     if c.get("SPLIT", c.get("SPLIT_K", 1)) < 1:
         raise ValueError(f"Invalid split-K: {where}")
+    if "M_SPLIT" in c or "TAIL" in c:
+        # gfx950 ring entry whose last rows run on a second configuration
+        tail = c.get("TAIL")
+        m1 = c.get("M_SPLIT")
+        if (entry["impl"] != "ring" or not isinstance(m1, int) or m1 < 1 or m1 % c["BLOCK_T"]
+                or not isinstance(tail, dict) or tail.get("impl") not in NATIVE
+                or "M_SPLIT" in tail.get("config", {})
+                or not _native_ok(tail["impl"], tail.get("config", {}), k)):
+            raise ValueError(f"Invalid row split: {where}")
     if entry["impl"] == "shortk" and k != 256:
         raise ValueError("shortk requires K=256")
     if c.get("MODE") == 3 and (c["NUM_STAGES"] < 4 or (k // 128) % (4 * c.get("SPLIT", 1))):

@@ -338,7 +338,26 @@ def skinny(A, B, As, Bs, config, **epilogue):
 
 def ring(A, B, As, Bs, config, **epilogue):
     """Large-tile kernel: direct-to-LDS ring, one barrier per K group.
-    K_FIXED=2 selects the K == 256 instance with both groups unrolled."""
+    K_FIXED=2 selects the K == 256 instance with both groups unrolled.
+
+    M_SPLIT / TAIL: rows [0, M_SPLIT) run on this configuration, filling whole
+    waves of workgroups over the CUs, and rows [M_SPLIT, M) run on the TAIL
+    entry ({"impl", "config"}) in a second launch.  That replaces a last, mostly
+    empty wave of big tiles; with M <= M_SPLIT the whole GEMM runs here."""
+    m1 = int(config.get("M_SPLIT", 0))
+    if m1 and A.shape[0] > m1 and "TAIL" in config:
+        import torch
+        from .engine import run
+        m, n = A.shape[0], B.shape[0]
+        out = epilogue.get("out")
+        C = torch.empty((m, n), device=A.device, dtype=torch.bfloat16) if out is None else out
+        head = {k: v for k, v in config.items() if k not in ("M_SPLIT", "TAIL")}
+        bias = epilogue.get("bias")
+        launch(A[:m1], B, As[:m1], Bs, _ring_cached(_freeze(head), int(head.get("K_FIXED", 0))),
+               bias=bias, out=C[:m1])
+        run(config["TAIL"], (A[m1:], B, As[m1:], Bs), bias=bias, out=C[m1:])
+        return C
+    config = {k: v for k, v in config.items() if k not in ("M_SPLIT", "TAIL")}
     return launch(A, B, As, Bs, _ring_cached(_freeze(config), int(config.get("K_FIXED", 0))),
                   **epilogue)
 
