@@ -115,6 +115,27 @@ __device__ __forceinline__ uint2 pack_bf16x4(const f32x4& v) {
     return o;
 }
 
+// The same for values known not to be NaN: the instruction alone.
+__device__ __forceinline__ uint2 pack_bf16x4_nonan(const f32x4& v) {
+    const f32x2 lo = {v[0], v[1]}, hi = {v[2], v[3]};
+    return make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2)),
+                      __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2)));
+}
+
+// True on every lane when some lane of the wave holds a NaN among the
+// tile's accumulators: one unordered compare covers two values.
+template <int NW, int NT>
+__device__ __forceinline__ bool wave_has_nan(const f32x4 (&acc)[NW][NT]) {
+    bool nan = false;
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            nan = nan | __builtin_isunordered(acc[w][t][0], acc[w][t][1]) |
+                  __builtin_isunordered(acc[w][t][2], acc[w][t][3]);
+    return __builtin_amdgcn_ballot_w64(nan) != 0;
+}
+
 // bf16 output of four consecutive columns n .. n+3, with the optional bias
 // added the way a separate bf16 `C + bias` does it: C is rounded to bf16
 // first, then bf16(C) + bias is evaluated in fp32 and rounded again.
@@ -651,14 +672,25 @@ void fp8bg_ring(KArgs a) {
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         unsigned char* region = lds + wave * (WTT * ROWB);
+        auto stage_c = [&](auto pack) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+            for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                const int row = t * 16 + r;
-                *(uint2*)(region + row * ROWB + (((2 * w + (qd >> 1)) ^ (row % CPR)) << 4) + (qd & 1) * 8) =
-                    out_bf16x4v(acc[w][t], a.bias != nullptr, bv[w]);
-            }
+                for (int w = 0; w < NW; ++w) {
+                    const int row = t * 16 + r;
+                    *(uint2*)(region + row * ROWB + (((2 * w + (qd >> 1)) ^ (row % CPR)) << 4) +
+                              (qd & 1) * 8) = pack(acc[w][t], bv[w]);
+                }
+        };
+        // Three copies of the packing loop, picked once per wave: with a
+        // bias; without, for a wave with no NaN accumulator (the conversion
+        // instruction alone); and without, canonicalising NaN.
+        if (a.bias)
+            stage_c([](const f32x4& v, uint2 b) { return out_bf16x4v(v, true, b); });
+        else if (!wave_has_nan(acc))
+            stage_c([](const f32x4& v, uint2) { return pack_bf16x4_nonan(v); });
+        else
+            stage_c([](const f32x4& v, uint2) { return pack_bf16x4(v); });
 #pragma unroll
         for (int h = 0; h < (WTT * CPR + 63) / 64; ++h) {
             const int idx = lane + 64 * h;
