@@ -604,18 +604,28 @@ void fp8bg_ring(KArgs a) {
 
         const unsigned char* st = lds + (i % ST) * STAGE;
         const float* sc = (const float*)(st + OPS);
-        const float sb = sc[TT + (w0 % 128 + wv_w * WTW) / 128];
+        // The group's first operands are read in the order the first token
+        // block's MFMAs consume them (token block 0, then weight blocks 0..NW-1),
+        // fenced so the LDS serves them in that order: the first MFMA waits
+        // for four reads, not for all of them (about 1% fewer cycles on the
+        // largest tiles, up to 4% on the mid-size ones).
+        i32x8 top = opread(st, TW + wv_t * WTT + (lane & 15));
+        __builtin_amdgcn_sched_barrier(0);
         i32x8 wop[NW];
 #pragma unroll
-        for (int w = 0; w < NW; ++w) wop[w] = opread(st, wv_w * WTW + w * 16 + (lane & 15));
+        for (int w = 0; w < NW; ++w) {
+            wop[w] = opread(st, wv_w * WTW + w * 16 + (lane & 15));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const float sb = sc[TT + (w0 % 128 + wv_w * WTW) / 128];
         // Software pipeline over token blocks: block t's products go into
         // their own registers, and each MFMA is followed by the four
         // promotion FMAs of the previous block's product for the same weight
         // block, which run on the VALU while the MFMA occupies the matrix
-        // pipe; block t + 1's operand is read from LDS one block ahead.  The
-        // scheduling fences keep this order (the default schedule promotes
-        // each product right after its own MFMA and stalls on it).
-        i32x8 top = opread(st, TW + wv_t * WTT + (lane & 15));
+        // pipe; block t + 1's operand is read from LDS one block ahead (for
+        // block 0, right after its first MFMA).  The scheduling fences keep
+        // this order (the default schedule promotes each product right after
+        // its own MFMA and stalls on it).
         float sa_t = sc[wv_t * WTT + (lane & 15)];
         f32x4 prev[NW];
         float s_prev = 0.f;
@@ -623,7 +633,7 @@ void fp8bg_ring(KArgs a) {
         for (int t = 0; t < NT; ++t) {
             i32x8 top_next = top;
             float sa_next = sa_t;
-            if (t + 1 < NT) {
+            if (t > 0 && t + 1 < NT) {
                 top_next = opread(st, TW + wv_t * WTT + (t + 1) * 16 + (lane & 15));
                 sa_next = sc[wv_t * WTT + (t + 1) * 16 + (lane & 15)];
             }
@@ -637,6 +647,11 @@ void fp8bg_ring(KArgs a) {
             for (int w = 0; w < NW; ++w) {
                 cur[w] = mfma16x16x128(wop[w], top);
                 if (t > 0) promote(acc[w][t - 1], prev[w], s_prev);
+                if (t == 0 && w == 0 && NT > 1) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    top_next = opread(st, TW + wv_t * WTT + 16 + (lane & 15));
+                    sa_next = sc[wv_t * WTT + 16 + (lane & 15)];
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
