@@ -458,14 +458,15 @@ void fp8bg_ring(KArgs a) {
     constexpr int NW = WTW / 16;
     constexpr int NT = WTT / 16;
     constexpr int ROWS = TW + TT;
-    constexpr int NJ = ROWS / (8 * NWAVE);        // 1 KB operand blocks per wave per group
+    constexpr int NBLK = ROWS / 8;                // 1 KB operand blocks (8 rows) per group
+    constexpr int NJ = (NBLK + NWAVE - 1) / NWAVE; // blocks per wave per group
     constexpr int NSC = ring_scale_slices(TW, TT, NWAVE);
     constexpr int NDMA = NJ + NSC;                // + the scale slices
     constexpr int OPS = ROWS * kRowBytes;         // operand bytes per stage
     constexpr int SCALES = NSC * NWAVE * 64;      // scale slots per stage
     constexpr int STAGE = OPS + SCALES * 4;
     static_assert(WTW % 16 == 0 && WTT % 16 == 0 && NW >= 1 && NT >= 1, "wave tile");
-    static_assert(ROWS % (8 * NWAVE) == 0 && NJ >= 1, "DMA blocks per wave");
+    static_assert(ROWS % 8 == 0 && NJ >= 1 && NJ * NWAVE - NBLK < NBLK, "DMA blocks per wave");
     constexpr int NBS = (TW + 127) / 128;         // Bs blocks the tile spans
     static_assert(TT + NBS + TW / 2 <= SCALES, "scale slots");
     // epilogue: 16 output rows of a wave at a time, staged in LDS
@@ -501,12 +502,20 @@ void fp8bg_ring(KArgs a) {
     int w0, t0;
     tile_origin(tile, a, w0, t0);
 
-    // ---- DMA sources: operand block b = wave * NJ + j holds rows 8b .. 8b+7 ----
+    // ---- DMA sources: operand block b holds rows 8b .. 8b+7; wave w moves
+    // blocks w * NJ .. w * NJ + NJ - 1.  When the NBLK blocks do not divide
+    // evenly among the waves, the indices past NBLK wrap to the first blocks:
+    // those are loaded twice, by two waves, into the same LDS bytes with the
+    // same data, so every wave issues NJ loads per group and the vmcnt
+    // bookkeeping stays uniform. ----
     const uint8_t* sbase[NJ];
     uint32_t soff[NJ];
+    int dblk[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-        const int b = wave * NJ + j;
+        const int b_raw = wave * NJ + j;
+        const int b = b_raw < NBLK ? b_raw : b_raw - NBLK;
+        dblk[j] = b;
         const int row = 8 * b + (lane >> 3);
         const int chunk = (lane & 7) ^ swz(row, a.swz);
         if (8 * b < TW) {
@@ -544,7 +553,7 @@ void fp8bg_ring(KArgs a) {
     auto dma_block = [&](int j, int g, int stage) {
         __builtin_amdgcn_global_load_lds(
             (const void*)(sbase[j] + (uint32_t)(soff[j] + (uint32_t)g * kGroupK)),
-            FP8BG_LDS_PTR(lds + stage * STAGE + (wave * NJ + j) * 1024), 16, 0, 0);
+            FP8BG_LDS_PTR(lds + stage * STAGE + dblk[j] * 1024), 16, 0, 0);
     };
     auto dma_scales = [&](int g, int stage) {
 #pragma unroll
@@ -1055,7 +1064,9 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(256, 128, 4, 2, 3, 0) X(256, 128, 4, 2, 2, 0) X(128, 256, 2, 4, 2, 0)    \
     X(256, 128, 4, 1, 2, 2) X(128, 128, 2, 2, 2, 2)                            \
     X(64, 64, 4, 1, 8, 0) X(128, 64, 4, 1, 6, 0) X(128, 32, 4, 1, 7, 0)        \
-    X(128, 128, 2, 2, 2, 0)
+    X(128, 128, 2, 2, 2, 0)                                                    \
+    X(192, 256, 3, 4, 2, 0) X(192, 128, 6, 2, 2, 0) X(192, 128, 6, 2, 3, 0)    \
+    X(192, 128, 3, 4, 3, 0) X(192, 64, 6, 2, 4, 0)
 
 // skinny with the fused activation quantiser: the 16-token (NT = 1) tiles
 // (4, 1, 8, 4) left out: with the bf16 staging it needs more than 256 VGPRs

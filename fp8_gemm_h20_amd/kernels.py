@@ -69,6 +69,10 @@ RING = (
     (256, 128, 4, 1, 2, 2), (128, 128, 2, 2, 2, 2),
     (64, 64, 4, 1, 8, 0), (128, 64, 4, 1, 6, 0), (128, 32, 4, 1, 7, 0),
     (128, 128, 2, 2, 2, 0),
+    # 192-row weight tiles, 12 waves (3 per SIMD): whole waves of tiles on 256
+    # CUs where N is a multiple of 192 (12288, 9216, 4608, 3072)
+    (192, 256, 3, 4, 2, 0), (192, 128, 6, 2, 2, 0), (192, 128, 6, 2, 3, 0),
+    (192, 128, 3, 4, 3, 0), (192, 64, 6, 2, 4, 0),
 )
 # back-compat name used by tests and the tuner
 INSTANCES = TILED
