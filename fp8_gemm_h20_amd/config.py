@@ -60,8 +60,11 @@ def _native_ok(impl, c, k):
     if impl == "ring":
         c = {key: v for key, v in c.items() if key not in ("M_SPLIT", "TAIL")}
         kf = c.get("K_FIXED", 0)
+        ku = c.get("K_UNROLL", 1)
+        split = c.get("SPLIT", 1) if c.get("SPLIT_MODE", "none") != "none" else 1
         return (c.get("SPLIT_MODE", "none") in _SPLIT_MODES and (kf == 0 or k == 256 * kf // 2) and
-                (tw, tt, c.get("WAVES_W"), c.get("WAVES_T"), c.get("STAGES"), kf) in RING)
+                (tw, tt, c.get("WAVES_W"), c.get("WAVES_T"), c.get("STAGES"), kf, ku) in RING and
+                (k // 128 // (split if (k // 128) % split == 0 else 1)) % ku == 0)
     if impl == "skinny":
         mode = c.get("SPLIT_MODE", "none")
         return (mode in ("none", "full") and

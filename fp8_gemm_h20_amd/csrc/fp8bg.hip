@@ -447,8 +447,12 @@ __device__ __forceinline__ void wait_vmcnt_lds() {
 // TT .. TT + TW/128 - 1).  ST stages form a ring: the loads of group
 // i + ST - 1 are issued while group i is computed, with no register staging
 // and no VGPR-destination memory loads in the loop, and each group needs one
-// barrier.
-template <int TW, int TT, int WW, int WT, int ST, int KF>
+// barrier.  With KU > 1 a barrier covers KU consecutive groups: the loads of
+// groups i + ST - KU .. i + ST - 1 refill the stages of the KU groups computed
+// before the barrier, and the second group's LDS reads overlap the first
+// group's MFMAs (small tiles spend most of a one-group step waiting for the
+// barrier and the first operand reads).
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU>
 __global__ __launch_bounds__(64 * WW * WT)
 __attribute__((amdgpu_waves_per_eu((WW * WT + 3) / 4, (WW * WT + 3) / 4)))
 void fp8bg_ring(KArgs a) {
@@ -474,7 +478,8 @@ void fp8bg_ring(KArgs a) {
     constexpr int CPR = ROWB / 16;                // 16-byte chunks per wave row
     static_assert(NWAVE * WTT * ROWB <= ST * STAGE, "epilogue regions inside the ring");
     static_assert(WTW <= 128 && 128 % WTW == 0, "wave weight rows inside one Bs block");
-    static_assert(ST >= 2 && NDMA * (ST - 2) < 64, "ring depth");
+    static_assert(KU >= 1 && ST >= 2 * KU && NDMA * (ST - 2 * KU) < 64, "ring depth");
+    static_assert(KF == 0 || KF % KU == 0, "groups per barrier");
     static_assert(ST * STAGE <= kMaxLds, "LDS");
 
     __shared__ __attribute__((aligned(1024))) unsigned char lds[ST * STAGE];
@@ -585,32 +590,19 @@ void fp8bg_ring(KArgs a) {
     // Every step issues its loads unconditionally so the vmcnt bookkeeping is
     // the same in every iteration: group indices past the range are clamped
     // to the last group (an L2 hit), and such a load lands in a stage that no
-    // later step reads (stage (i + ST - 1) % ST with i + ST - 1 >= kcount is
-    // only read again at step i + ST - 1).
+    // later step reads (the stage of group g is read only by group g, and a
+    // clamped index g is past the last group).
     const int g_last = k_lo + kcount - 1;
 #pragma unroll
-    for (int s = 0; s < ST - 1; ++s) dma(min(k_lo + s, g_last), s);
+    for (int s = 0; s < ST - KU; ++s) dma(min(k_lo + s, g_last), s);
 
-#pragma unroll (KF ? KF : 1)
-    for (int i = 0; i < kcount; ++i) {
-        // Stage i is complete once at most the DMA instructions of the ST - 2
-        // later steps are outstanding (vmcnt retires in issue order); this
-        // wave's LDS reads of stage (i - 1) % ST have all returned.
-        wait_vmcnt_lds<NDMA * (ST - 2)>();
-        // All waves' blocks of stage i have landed, and every wave is done
-        // reading stage (i - 1) % ST, which is refilled next.  The empty asm
-        // statements keep the compiler from moving LDS reads or writes
-        // across the barrier.
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        // Loads of group i + ST - 1, spread over the token-block loop below:
-        // operand block j before token block j * NT / (2 NJ), the scale
-        // slices before token block NT / 2.  Issued together right after the
-        // barrier, the waves' loads queue at the address unit and hold back
-        // the first MFMAs; spread out, they overlap the MFMA stream.
-        const int g_next = min(k_lo + i + ST - 1, g_last), s_next = (i + ST - 1) % ST;
-
+    // One 128-K group: stage i % ST is computed while the loads of group
+    // g_next are spread over its token blocks (operand block j before token
+    // block j * NT / (2 NJ), the scale slices before token block NT / 2).
+    // Issued together right after the barrier, the waves' loads queue at the
+    // address unit and hold back the first MFMAs; spread out, they overlap
+    // the MFMA stream.
+    auto group = [&](int i, int g_next, int s_next) {
         const unsigned char* st = lds + (i % ST) * STAGE;
         const float* sc = (const float*)(st + OPS);
         // The group's first operands are read in the order the first token
@@ -671,8 +663,30 @@ void fp8bg_ring(KArgs a) {
         }
 #pragma unroll
         for (int w = 0; w < NW; ++w) promote(acc[w][NT - 1], prev[w], s_prev);
+    };
+
+#pragma unroll (KF ? KF / KU : 1)
+    for (int i = 0; i < kcount; i += KU) {
+        // Groups i .. i + KU - 1 are complete once at most the DMA
+        // instructions of the ST - 2 KU later groups are outstanding (vmcnt
+        // retires in issue order); this wave's LDS reads of the KU groups
+        // before have all returned.
+        wait_vmcnt_lds<NDMA * (ST - 2 * KU)>();
+        // All waves' blocks of those stages have landed, and every wave is
+        // done reading the stages of groups i - KU .. i - 1, which are
+        // refilled next.  The empty asm statements keep the compiler from
+        // moving LDS reads or writes across the barrier.
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+            // group i + ST - KU + u refills the stage of group i - KU + u
+            const int g = i + ST - KU + u;
+            group(i + u, min(k_lo + g, g_last), g % ST);
+        }
     }
-    // The clamped loads of the last ST - 1 steps are still in flight: they
+    // The clamped loads of the last ST - KU groups are still in flight: they
     // must land before the LDS is reused below or handed to another workgroup.
     wait_vmcnt<0>();
 
@@ -1055,18 +1069,25 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(2, 4, 4, 2) X(2, 4, 8, 1) X(2, 4, 8, 2)                                  \
     X(4, 4, 4, 1) X(4, 4, 8, 1) X(4, 4, 4, 2)
 
-// ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed)
+// ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier)
 #define FP8BG_RING(X)                                                          \
-    X(256, 128, 4, 1, 3, 0) X(256, 128, 2, 2, 3, 0) X(128, 128, 2, 2, 4, 0)    \
-    X(128, 128, 4, 1, 4, 0) X(128, 128, 2, 2, 3, 0) X(128, 64, 2, 2, 4, 0)     \
-    X(128, 64, 4, 1, 4, 0) X(128, 64, 2, 2, 3, 0) X(64, 64, 4, 1, 4, 0)        \
-    X(256, 64, 4, 1, 3, 0) X(128, 32, 4, 1, 4, 0) X(256, 256, 4, 2, 2, 0)      \
-    X(256, 128, 4, 2, 3, 0) X(256, 128, 4, 2, 2, 0) X(128, 256, 2, 4, 2, 0)    \
-    X(256, 128, 4, 1, 2, 2) X(128, 128, 2, 2, 2, 2)                            \
-    X(64, 64, 4, 1, 8, 0) X(128, 64, 4, 1, 6, 0) X(128, 32, 4, 1, 7, 0)        \
-    X(128, 128, 2, 2, 2, 0)                                                    \
-    X(192, 256, 3, 4, 2, 0) X(192, 128, 6, 2, 2, 0) X(192, 128, 6, 2, 3, 0)    \
-    X(192, 128, 3, 4, 3, 0) X(192, 64, 6, 2, 4, 0)
+    X(256, 128, 4, 1, 3, 0, 1) X(256, 128, 2, 2, 3, 0, 1)                      \
+    X(128, 128, 2, 2, 4, 0, 1) X(128, 128, 4, 1, 4, 0, 1)                      \
+    X(128, 128, 2, 2, 3, 0, 1) X(128, 64, 2, 2, 4, 0, 1)                       \
+    X(128, 64, 4, 1, 4, 0, 1) X(128, 64, 2, 2, 3, 0, 1) X(64, 64, 4, 1, 4, 0, 1) \
+    X(256, 64, 4, 1, 3, 0, 1) X(128, 32, 4, 1, 4, 0, 1)                        \
+    X(256, 256, 4, 2, 2, 0, 1) X(256, 128, 4, 2, 3, 0, 1)                      \
+    X(256, 128, 4, 2, 2, 0, 1) X(128, 256, 2, 4, 2, 0, 1)                      \
+    X(256, 128, 4, 1, 2, 2, 1) X(128, 128, 2, 2, 2, 2, 1)                      \
+    X(64, 64, 4, 1, 8, 0, 1) X(128, 64, 4, 1, 6, 0, 1) X(128, 32, 4, 1, 7, 0, 1) \
+    X(128, 128, 2, 2, 2, 0, 1)                                                 \
+    X(192, 256, 3, 4, 2, 0, 1) X(192, 128, 6, 2, 2, 0, 1)                      \
+    X(192, 128, 6, 2, 3, 0, 1) X(192, 128, 3, 4, 3, 0, 1)                      \
+    X(192, 64, 6, 2, 4, 0, 1)                                                  \
+    X(64, 64, 4, 1, 4, 0, 2) X(64, 64, 4, 1, 8, 0, 2) X(64, 64, 4, 1, 8, 0, 4) \
+    X(128, 64, 4, 1, 4, 0, 2) X(128, 64, 4, 1, 6, 0, 2)                        \
+    X(128, 32, 4, 1, 4, 0, 2) X(128, 32, 4, 1, 7, 0, 2)                        \
+    X(128, 64, 2, 2, 4, 0, 2) X(192, 64, 6, 2, 4, 0, 2)
 
 // skinny with the fused activation quantiser: the 16-token (NT = 1) tiles
 // (4, 1, 8, 4) left out: with the bf16 staging it needs more than 256 VGPRs
@@ -1104,11 +1125,11 @@ FP8BG_SKINNY(FP8BG_SKINNY_LAUNCHER)
 FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_LAUNCHER)
 #undef FP8BG_SKINNY_QA_LAUNCHER
 
-#define FP8BG_RING_LAUNCHER(TW, TT, WW, WT, ST, KF)                                          \
-    static void ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF(dim3 g, size_t shm,            \
-                                                             hipStream_t s, const KArgs& a) { \
-        hipLaunchKernelGGL((fp8bg_ring<TW, TT, WW, WT, ST, KF>), g, dim3(64 * WW * WT), shm, \
-                           s, a);                                                             \
+#define FP8BG_RING_LAUNCHER(TW, TT, WW, WT, ST, KF, KU)                                      \
+    static void ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF##_##KU(                          \
+        dim3 g, size_t shm, hipStream_t s, const KArgs& a) {                                  \
+        hipLaunchKernelGGL((fp8bg_ring<TW, TT, WW, WT, ST, KF, KU>), g, dim3(64 * WW * WT),  \
+                           shm, s, a);                                                        \
     }
 FP8BG_RING(FP8BG_RING_LAUNCHER)
 #undef FP8BG_RING_LAUNCHER
@@ -1117,9 +1138,9 @@ FP8BG_RING(FP8BG_RING_LAUNCHER)
     {FP8BG_KIND_TILED, TW, TT, WW, WT, 1, 1, 1, KF, kThreads, tiled_##TW##_##TT##_##WW##_##WT##_##KF},
 #define FP8BG_SKINNY_ENTRY(NW, NT, S, U) \
     {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 1, 0, 64 * S, skinny_##NW##_##NT##_##S##_##U},
-#define FP8BG_RING_ENTRY(TW, TT, WW, WT, ST, KF)                                  \
-    {FP8BG_KIND_RING, TW, TT, WW, WT, 1, 1, ST, KF, 64 * WW * WT,                 \
-     ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF},
+#define FP8BG_RING_ENTRY(TW, TT, WW, WT, ST, KF, KU)                              \
+    {FP8BG_KIND_RING, TW, TT, WW, WT, 1, KU, ST, KF, 64 * WW * WT,                \
+     ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF##_##KU},
 const Instance kInstances[] = {FP8BG_TILED(FP8BG_TILED_ENTRY) FP8BG_SKINNY(FP8BG_SKINNY_ENTRY)
                                    FP8BG_RING(FP8BG_RING_ENTRY)};
 #define FP8BG_SKINNY_QA_ENTRY(NW, NT, S, U) \
@@ -1161,7 +1182,7 @@ int find_instance(const fp8bg_config* c) {
             c->k_fixed == 0)
             return i;
         if (k.kind == FP8BG_KIND_RING && k.ww == c->waves_w && k.wt == c->waves_t &&
-            k.stages == c->stages && k.kf == c->k_fixed)
+            k.stages == c->stages && k.kf == c->k_fixed && k.unroll == max(c->unroll, 1))
             return i;
     }
     return -1;
@@ -1230,6 +1251,9 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     int64_t n_split = 0;
     if (split > 1) n_split = cfg->split_mode == FP8BG_SPLIT_TAIL ? tiles % num_cus : tiles;
     if (n_split == 0) split = 1;
+    // a ring kernel computing KU groups per barrier needs whole multiples of
+    // KU in every workgroup's K range (kg / split divides kg)
+    if (ring && (kg / split) % k.unroll) return FP8BG_ERR_CONFIG;
     const int64_t n_dp = tiles - n_split;
     const int64_t grid = n_dp + n_split * split;
     if (grid > 0x7fffffff) return FP8BG_ERR_SHAPE;

@@ -97,7 +97,9 @@ typedef struct fp8bg_config {
     int32_t waves_w;    /* tiled/ring: waves along N inside the tile */
     int32_t waves_t;    /* tiled/ring: waves along M inside the tile */
     int32_t waves_k;    /* skinny: waves splitting K inside a workgroup (4 or 8) */
-    int32_t unroll;     /* skinny: 128-K groups in flight per wave */
+    int32_t unroll;     /* skinny: 128-K groups in flight per wave;
+                           ring: 128-K groups per barrier (1, 2 or 4; 0 means 1);
+                           K/128/split must be a multiple of it */
     int32_t stages;     /* ring: LDS ring depth in 128-K groups */
     int32_t split;      /* cross-workgroup K split factor, in 128-K groups;
                            normalised to 1 when it does not divide K/128
