@@ -63,7 +63,8 @@ def _native_ok(impl, c, k):
         ku = c.get("K_UNROLL", 1)
         split = c.get("SPLIT", 1) if c.get("SPLIT_MODE", "none") != "none" else 1
         return (c.get("SPLIT_MODE", "none") in _SPLIT_MODES and (kf == 0 or k == 256 * kf // 2) and
-                (tw, tt, c.get("WAVES_W"), c.get("WAVES_T"), c.get("STAGES"), kf, ku) in RING and
+                (tw, tt, c.get("WAVES_W"), c.get("WAVES_T"), c.get("STAGES"), kf, ku,
+                 c.get("WAVES_K", 1)) in RING and
                 (k // 128 // (split if (k // 128) % split == 0 else 1)) % ku == 0)
     if impl == "skinny":
         mode = c.get("SPLIT_MODE", "none")

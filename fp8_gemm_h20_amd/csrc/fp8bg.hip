@@ -457,12 +457,18 @@ struct WaveRole {
 // groups i + ST - KU .. i + ST - 1 refill the stages of the KU groups computed
 // before the barrier, and the second group's LDS reads overlap the first
 // group's MFMAs (small tiles spend most of a one-group step waiting for the
-// barrier and the first operand reads).
-template <int TW, int TT, int WW, int WT, int ST, int KF, int KU>
-__global__ __launch_bounds__(64 * WW * WT)
-__attribute__((amdgpu_waves_per_eu((WW * WT + 3) / 4, (WW * WT + 3) / 4)))
+// barrier and the first operand reads).  With WK > 1 the workgroup holds WK
+// slices of WW x WT waves; slice k computes (and loads) the groups i with
+// i % WK == k, in the stages s with s % WK == k, so each slice runs its own
+// ring of ST / WK stages and KU / WK groups per barrier.  The slices' partial
+// tiles are summed through LDS in fixed slice order at the end: for tiles
+// with few workgroups and long K (narrow N at small M), WK times the loads
+// and MFMAs in flight without a second launch.
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK>
+__global__ __launch_bounds__(64 * WW * WT * WK)
+__attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
 void fp8bg_ring(KArgs a) {
-    constexpr int NWAVE = WW * WT;
+    constexpr int NWAVE = WW * WT;                // waves of one K slice
     constexpr int WTW = TW / WW;
     constexpr int WTT = TT / WT;
     constexpr int NW = WTW / 16;
@@ -484,14 +490,18 @@ void fp8bg_ring(KArgs a) {
     constexpr int CPR = ROWB / 16;                // 16-byte chunks per wave row
     static_assert(NWAVE * WTT * ROWB <= ST * STAGE, "epilogue regions inside the ring");
     static_assert(WTW <= 128 && 128 % WTW == 0, "wave weight rows inside one Bs block");
-    static_assert(KU >= 1 && ST >= 2 * KU && NDMA * (ST - 2 * KU) < 64, "ring depth");
+    static_assert(KU >= 1 && ST >= 2 * KU && NDMA * (ST - 2 * KU) / WK < 64, "ring depth");
     static_assert(KF == 0 || KF % KU == 0, "groups per barrier");
+    static_assert(WK >= 1 && ST % WK == 0 && KU % WK == 0 && (WK == 1 || KF == 0), "K slices");
+    static_assert((WK - 1) * TW * TT * 4 <= ST * STAGE, "slice reduction inside the ring");
     static_assert(ST * STAGE <= kMaxLds, "LDS");
 
     __shared__ __attribute__((aligned(1024))) unsigned char lds[ST * STAGE];
 
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ks = wave_all / NWAVE;              // K slice
+    const int wave = wave_all % NWAVE;            // wave inside the slice
     const int wv_w = wave % WW, wv_t = wave / WW;
 
     // ---- tile decode ----
@@ -599,8 +609,7 @@ void fp8bg_ring(KArgs a) {
     // later step reads (the stage of group g is read only by group g, and a
     // clamped index g is past the last group).
     const int g_last = k_lo + kcount - 1;
-#pragma unroll
-    for (int s = 0; s < ST - KU; ++s) dma(min(k_lo + s, g_last), s);
+    for (int s = ks; s < ST - KU; s += WK) dma(min(k_lo + s, g_last), s);
 
     // One 128-K group: stage i % ST is computed while the loads of group
     // g_next are spread over its token blocks (operand block j before token
@@ -693,9 +702,10 @@ void fp8bg_ring(KArgs a) {
     for (int i = 0; i < kcount; i += KU) {
         // Groups i .. i + KU - 1 are complete once at most the DMA
         // instructions of the ST - 2 KU later groups are outstanding (vmcnt
-        // retires in issue order); this wave's LDS reads of the KU groups
-        // before have all returned.
-        wait_vmcnt_lds<NDMA * (ST - 2 * KU)>();
+        // retires in issue order; a wave loads only its slice's groups, 1 in
+        // WK); this wave's LDS reads of the KU groups before have all
+        // returned.
+        wait_vmcnt_lds<NDMA * (ST - 2 * KU) / WK>();
         // All waves' blocks of those stages have landed, and every wave is
         // done reading the stages of groups i - KU .. i - 1, which are
         // refilled next.  The empty asm statements keep the compiler from
@@ -704,8 +714,10 @@ void fp8bg_ring(KArgs a) {
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
 #pragma unroll
-        for (int u = 0; u < KU; ++u) {
-            // group i + ST - KU + u refills the stage of group i - KU + u
+        for (int uk = 0; uk < KU / WK; ++uk) {
+            // group i + ST - KU + u refills the stage of group i - KU + u;
+            // both belong to this wave's slice
+            const int u = uk * WK + ks;
             const int g = i + ST - KU + u;
             group(i + u, min(k_lo + g, g_last), g % ST, role);
         }
@@ -724,24 +736,64 @@ void fp8bg_ring(KArgs a) {
     wait_vmcnt<0>();
 
     // ---- epilogue ----
-    if (blockIdx.x < a.n_dp) {
-        // bf16 C through LDS: once every wave has passed the barrier below the
-        // whole ring is free, and each wave writes its WTT x WTW tile into its
-        // own region (row-major, chunk c of row r at slot c ^ (r % CPR)),
-        // reads it back as whole 16-byte chunks and stores full 128-byte
-        // lines with non-temporal stores (C is not re-read).  The bias row
-        // sits in the last stage's scale area, so it is read first.
+    const bool dp = blockIdx.x < a.n_dp;
+    const int r = lane & 15, qd = lane >> 4;
+    // The bias row sits in the last group's scale area: read it before the
+    // LDS is reused.
+    uint2 bv[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) bv[w] = (uint2){0u, 0u};
+    if (dp) {
         const uint16_t* bl = (const uint16_t*)(lds + ((kcount - 1) % ST) * STAGE + OPS +
                                                (TT + NBS) * 4);
-        const int r = lane & 15, qd = lane >> 4;
-        uint2 bv[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w)
             bv[w] = *(const uint2*)(bl + wv_w * WTW + w * 16 + qd * 4);
+    }
+    if (WK > 1) {
+        // slices 1 .. WK-1 park their partial tiles in the (now free) ring;
+        // slice 0 adds them in slice order
+        f32x4* red = (f32x4*)lds;
         wait_vmcnt_lds<0>();
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
+        if (ks > 0) {
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    red[(((ks - 1) * NWAVE + wave) * NW * NT + w * NT + t) * 64 + lane] = acc[w][t];
+        }
+        wait_vmcnt_lds<0>();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (ks == 0) {
+            for (int k2 = 1; k2 < WK; ++k2)
+#pragma unroll
+                for (int w = 0; w < NW; ++w)
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        const f32x4 v = red[(((k2 - 1) * NWAVE + wave) * NW * NT + w * NT + t) * 64 + lane];
+                        acc[w][t][0] += v[0];
+                        acc[w][t][1] += v[1];
+                        acc[w][t][2] += v[2];
+                        acc[w][t][3] += v[3];
+                    }
+        }
+    }
+    if (dp) {
+        // bf16 C through LDS: once every wave has passed the barrier below the
+        // whole ring is free, and each wave of slice 0 writes its WTT x WTW
+        // tile into its own region (row-major, chunk c of row r at slot
+        // c ^ (r % CPR)), reads it back as whole 16-byte chunks and stores
+        // full 128-byte lines with non-temporal stores (C is not re-read).
+        wait_vmcnt_lds<0>();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (ks > 0) return;
         unsigned char* region = lds + wave * (WTT * ROWB);
         auto stage_c = [&](auto pack) {
 #pragma unroll
@@ -774,6 +826,7 @@ void fp8bg_ring(KArgs a) {
         }
         return;
     }
+    if (ks > 0) return;
     float* mine = a.ws + ((size_t)(tile - a.n_dp) * a.split + sidx) * (size_t)(TW * TT);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -1102,25 +1155,30 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(2, 4, 4, 2) X(2, 4, 8, 1) X(2, 4, 8, 2)                                  \
     X(4, 4, 4, 1) X(4, 4, 8, 1) X(4, 4, 4, 2)
 
-// ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier)
-#define FP8BG_RING(X)                                                          \
-    X(256, 128, 4, 1, 3, 0, 1) X(256, 128, 2, 2, 3, 0, 1)                      \
-    X(128, 128, 2, 2, 4, 0, 1) X(128, 128, 4, 1, 4, 0, 1)                      \
-    X(128, 128, 2, 2, 3, 0, 1) X(128, 64, 2, 2, 4, 0, 1)                       \
-    X(128, 64, 4, 1, 4, 0, 1) X(128, 64, 2, 2, 3, 0, 1) X(64, 64, 4, 1, 4, 0, 1) \
-    X(256, 64, 4, 1, 3, 0, 1) X(128, 32, 4, 1, 4, 0, 1)                        \
-    X(256, 256, 4, 2, 2, 0, 1) X(256, 128, 4, 2, 3, 0, 1)                      \
-    X(256, 128, 4, 2, 2, 0, 1) X(128, 256, 2, 4, 2, 0, 1)                      \
-    X(256, 128, 4, 1, 2, 2, 1) X(128, 128, 2, 2, 2, 2, 1)                      \
-    X(64, 64, 4, 1, 8, 0, 1) X(128, 64, 4, 1, 6, 0, 1) X(128, 32, 4, 1, 7, 0, 1) \
-    X(128, 128, 2, 2, 2, 0, 1)                                                 \
-    X(192, 256, 3, 4, 2, 0, 1) X(192, 128, 6, 2, 2, 0, 1)                      \
-    X(192, 128, 6, 2, 3, 0, 1) X(192, 128, 3, 4, 3, 0, 1)                      \
-    X(192, 64, 6, 2, 4, 0, 1)                                                  \
-    X(64, 64, 4, 1, 4, 0, 2) X(64, 64, 4, 1, 8, 0, 2) X(64, 64, 4, 1, 8, 0, 4) \
-    X(128, 64, 4, 1, 4, 0, 2) X(128, 64, 4, 1, 6, 0, 2)                        \
-    X(128, 32, 4, 1, 4, 0, 2) X(128, 32, 4, 1, 7, 0, 2)                        \
-    X(128, 64, 2, 2, 4, 0, 2) X(192, 64, 6, 2, 4, 0, 2)
+// ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
+//        K slices)
+#define FP8BG_RING(X)                                           \
+    X(256, 128, 4, 1, 3, 0, 1, 1) X(256, 128, 2, 2, 3, 0, 1, 1) \
+    X(128, 128, 2, 2, 4, 0, 1, 1) X(128, 128, 4, 1, 4, 0, 1, 1) \
+    X(128, 128, 2, 2, 3, 0, 1, 1) X(128, 64, 2, 2, 4, 0, 1, 1)  \
+    X(128, 64, 4, 1, 4, 0, 1, 1) X(128, 64, 2, 2, 3, 0, 1, 1)   \
+    X(64, 64, 4, 1, 4, 0, 1, 1) X(256, 64, 4, 1, 3, 0, 1, 1)    \
+    X(128, 32, 4, 1, 4, 0, 1, 1) X(256, 256, 4, 2, 2, 0, 1, 1)  \
+    X(256, 128, 4, 2, 3, 0, 1, 1) X(256, 128, 4, 2, 2, 0, 1, 1) \
+    X(128, 256, 2, 4, 2, 0, 1, 1) X(256, 128, 4, 1, 2, 2, 1, 1) \
+    X(128, 128, 2, 2, 2, 2, 1, 1) X(64, 64, 4, 1, 8, 0, 1, 1)   \
+    X(128, 64, 4, 1, 6, 0, 1, 1) X(128, 32, 4, 1, 7, 0, 1, 1)   \
+    X(128, 128, 2, 2, 2, 0, 1, 1) X(192, 256, 3, 4, 2, 0, 1, 1) \
+    X(192, 128, 6, 2, 2, 0, 1, 1) X(192, 128, 6, 2, 3, 0, 1, 1) \
+    X(192, 128, 3, 4, 3, 0, 1, 1) X(192, 64, 6, 2, 4, 0, 1, 1)  \
+    X(64, 64, 4, 1, 4, 0, 2, 1) X(64, 64, 4, 1, 8, 0, 2, 1)     \
+    X(64, 64, 4, 1, 8, 0, 4, 1) X(128, 64, 4, 1, 4, 0, 2, 1)    \
+    X(128, 64, 4, 1, 6, 0, 2, 1) X(128, 32, 4, 1, 4, 0, 2, 1)   \
+    X(128, 32, 4, 1, 7, 0, 2, 1) X(128, 64, 2, 2, 4, 0, 2, 1)   \
+    X(192, 64, 6, 2, 4, 0, 2, 1) X(64, 64, 4, 1, 4, 0, 2, 2)    \
+    X(64, 64, 4, 1, 8, 0, 2, 2) X(64, 64, 4, 1, 8, 0, 4, 2)     \
+    X(64, 64, 4, 1, 8, 0, 4, 4) X(128, 64, 4, 1, 6, 0, 2, 2)    \
+    X(128, 32, 4, 1, 4, 0, 2, 2)
 
 // skinny with the fused activation quantiser: the 16-token (NT = 1) tiles
 // (4, 1, 8, 4) left out: with the bf16 staging it needs more than 256 VGPRs
@@ -1158,11 +1216,11 @@ FP8BG_SKINNY(FP8BG_SKINNY_LAUNCHER)
 FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_LAUNCHER)
 #undef FP8BG_SKINNY_QA_LAUNCHER
 
-#define FP8BG_RING_LAUNCHER(TW, TT, WW, WT, ST, KF, KU)                                      \
-    static void ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF##_##KU(                          \
+#define FP8BG_RING_LAUNCHER(TW, TT, WW, WT, ST, KF, KU, WK)                                  \
+    static void ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF##_##KU##_##WK(                   \
         dim3 g, size_t shm, hipStream_t s, const KArgs& a) {                                  \
-        hipLaunchKernelGGL((fp8bg_ring<TW, TT, WW, WT, ST, KF, KU>), g, dim3(64 * WW * WT),  \
-                           shm, s, a);                                                        \
+        hipLaunchKernelGGL((fp8bg_ring<TW, TT, WW, WT, ST, KF, KU, WK>), g,                  \
+                           dim3(64 * WW * WT * WK), shm, s, a);                               \
     }
 FP8BG_RING(FP8BG_RING_LAUNCHER)
 #undef FP8BG_RING_LAUNCHER
@@ -1171,9 +1229,9 @@ FP8BG_RING(FP8BG_RING_LAUNCHER)
     {FP8BG_KIND_TILED, TW, TT, WW, WT, 1, 1, 1, KF, kThreads, tiled_##TW##_##TT##_##WW##_##WT##_##KF},
 #define FP8BG_SKINNY_ENTRY(NW, NT, S, U) \
     {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 1, 0, 64 * S, skinny_##NW##_##NT##_##S##_##U},
-#define FP8BG_RING_ENTRY(TW, TT, WW, WT, ST, KF, KU)                              \
-    {FP8BG_KIND_RING, TW, TT, WW, WT, 1, KU, ST, KF, 64 * WW * WT,                \
-     ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF##_##KU},
+#define FP8BG_RING_ENTRY(TW, TT, WW, WT, ST, KF, KU, WK)                          \
+    {FP8BG_KIND_RING, TW, TT, WW, WT, WK, KU, ST, KF, 64 * WW * WT * WK,          \
+     ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF##_##KU##_##WK},
 const Instance kInstances[] = {FP8BG_TILED(FP8BG_TILED_ENTRY) FP8BG_SKINNY(FP8BG_SKINNY_ENTRY)
                                    FP8BG_RING(FP8BG_RING_ENTRY)};
 #define FP8BG_SKINNY_QA_ENTRY(NW, NT, S, U) \
@@ -1215,7 +1273,8 @@ int find_instance(const fp8bg_config* c) {
             c->k_fixed == 0)
             return i;
         if (k.kind == FP8BG_KIND_RING && k.ww == c->waves_w && k.wt == c->waves_t &&
-            k.stages == c->stages && k.kf == c->k_fixed && k.unroll == max(c->unroll, 1))
+            k.stages == c->stages && k.kf == c->k_fixed && k.unroll == max(c->unroll, 1) &&
+            k.wk == max(c->waves_k, 1))
             return i;
     }
     return -1;

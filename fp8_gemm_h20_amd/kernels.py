@@ -16,7 +16,7 @@ Two families of config dicts are accepted:
     GROUP_SIZE_M, SCALE_LDS, XCD_REMAP, LDS_SWIZZLE (LDS-tiled kernel);
   - impl "skinny": BLOCK_W, BLOCK_T, WAVES_K, UNROLL, SPLIT, SPLIT_MODE,
     XCD_REMAP (small-M kernel, waves split K);
-  - impl "ring": BLOCK_W, BLOCK_T, WAVES_W, WAVES_T, STAGES, K_UNROLL, SPLIT,
+  - impl "ring": BLOCK_W, BLOCK_T, WAVES_W, WAVES_T, STAGES, K_UNROLL, WAVES_K, SPLIT,
     SPLIT_MODE, GROUP_SIZE_M, XCD_REMAP, LDS_SWIZZLE (direct-to-LDS ring
     kernel);
   - impl "shortk": BLOCK_W, BLOCK_T (K == 256, no K loop).
@@ -59,25 +59,31 @@ SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
 # skinny with the activation quantiser fused (16-token tiles, except the one
 # that would spill); must match FP8BG_SKINNY_QA in csrc/fp8bg.hip
 SKINNY_QA = tuple(c for c in SKINNY if c[1] == 1 and c != (4, 1, 8, 4))
-# ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier)
+# ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
+#        K slices)
 RING = (
-    (256, 128, 4, 1, 3, 0, 1), (256, 128, 2, 2, 3, 0, 1), (128, 128, 2, 2, 4, 0, 1),
-    (128, 128, 4, 1, 4, 0, 1), (128, 128, 2, 2, 3, 0, 1), (128, 64, 2, 2, 4, 0, 1),
-    (128, 64, 4, 1, 4, 0, 1), (128, 64, 2, 2, 3, 0, 1), (64, 64, 4, 1, 4, 0, 1),
-    (256, 64, 4, 1, 3, 0, 1), (128, 32, 4, 1, 4, 0, 1), (256, 256, 4, 2, 2, 0, 1),
-    (256, 128, 4, 2, 3, 0, 1), (256, 128, 4, 2, 2, 0, 1), (128, 256, 2, 4, 2, 0, 1),
-    (256, 128, 4, 1, 2, 2, 1), (128, 128, 2, 2, 2, 2, 1),
-    (64, 64, 4, 1, 8, 0, 1), (128, 64, 4, 1, 6, 0, 1), (128, 32, 4, 1, 7, 0, 1),
-    (128, 128, 2, 2, 2, 0, 1),
+    (256, 128, 4, 1, 3, 0, 1, 1), (256, 128, 2, 2, 3, 0, 1, 1), (128, 128, 2, 2, 4, 0, 1, 1),
+    (128, 128, 4, 1, 4, 0, 1, 1), (128, 128, 2, 2, 3, 0, 1, 1), (128, 64, 2, 2, 4, 0, 1, 1),
+    (128, 64, 4, 1, 4, 0, 1, 1), (128, 64, 2, 2, 3, 0, 1, 1), (64, 64, 4, 1, 4, 0, 1, 1),
+    (256, 64, 4, 1, 3, 0, 1, 1), (128, 32, 4, 1, 4, 0, 1, 1), (256, 256, 4, 2, 2, 0, 1, 1),
+    (256, 128, 4, 2, 3, 0, 1, 1), (256, 128, 4, 2, 2, 0, 1, 1), (128, 256, 2, 4, 2, 0, 1, 1),
+    (256, 128, 4, 1, 2, 2, 1, 1), (128, 128, 2, 2, 2, 2, 1, 1),
+    (64, 64, 4, 1, 8, 0, 1, 1), (128, 64, 4, 1, 6, 0, 1, 1), (128, 32, 4, 1, 7, 0, 1, 1),
+    (128, 128, 2, 2, 2, 0, 1, 1),
     # 192-row weight tiles, 12 waves (3 per SIMD): whole waves of tiles on 256
     # CUs where N is a multiple of 192 (12288, 9216, 4608, 3072)
-    (192, 256, 3, 4, 2, 0, 1), (192, 128, 6, 2, 2, 0, 1), (192, 128, 6, 2, 3, 0, 1),
-    (192, 128, 3, 4, 3, 0, 1), (192, 64, 6, 2, 4, 0, 1),
+    (192, 256, 3, 4, 2, 0, 1, 1), (192, 128, 6, 2, 2, 0, 1, 1), (192, 128, 6, 2, 3, 0, 1, 1),
+    (192, 128, 3, 4, 3, 0, 1, 1), (192, 64, 6, 2, 4, 0, 1, 1),
     # small tiles with two (or four) 128-K groups per barrier
-    (64, 64, 4, 1, 4, 0, 2), (64, 64, 4, 1, 8, 0, 2), (64, 64, 4, 1, 8, 0, 4),
-    (128, 64, 4, 1, 4, 0, 2), (128, 64, 4, 1, 6, 0, 2),
-    (128, 32, 4, 1, 4, 0, 2), (128, 32, 4, 1, 7, 0, 2),
-    (128, 64, 2, 2, 4, 0, 2), (192, 64, 6, 2, 4, 0, 2),
+    (64, 64, 4, 1, 4, 0, 2, 1), (64, 64, 4, 1, 8, 0, 2, 1), (64, 64, 4, 1, 8, 0, 4, 1),
+    (128, 64, 4, 1, 4, 0, 2, 1), (128, 64, 4, 1, 6, 0, 2, 1),
+    (128, 32, 4, 1, 4, 0, 2, 1), (128, 32, 4, 1, 7, 0, 2, 1),
+    (128, 64, 2, 2, 4, 0, 2, 1), (192, 64, 6, 2, 4, 0, 2, 1),
+    # K slices: two (or four) groups of waves split a tile's K groups and sum
+    # their partial tiles through LDS (narrow N, long K, few workgroups)
+    (64, 64, 4, 1, 4, 0, 2, 2), (64, 64, 4, 1, 8, 0, 2, 2),
+    (64, 64, 4, 1, 8, 0, 4, 2), (64, 64, 4, 1, 8, 0, 4, 4),
+    (128, 64, 4, 1, 6, 0, 2, 2), (128, 32, 4, 1, 4, 0, 2, 2),
 )
 # back-compat name used by tests and the tuner
 INSTANCES = TILED
@@ -157,9 +163,11 @@ def skinny_struct(cfg):
 
 
 def ring_struct(cfg, k_fixed=0):
-    """C config struct for a ring config dict (K_UNROLL: 128-K groups per barrier)."""
+    """C config struct for a ring config dict (K_UNROLL: 128-K groups per
+    barrier; WAVES_K: K slices of waves)."""
     return _lib.Config(_lib.KIND_RING, int(cfg["BLOCK_W"]), int(cfg["BLOCK_T"]),
-                       int(cfg["WAVES_W"]), int(cfg["WAVES_T"]), 1, int(cfg.get("K_UNROLL", 1)),
+                       int(cfg["WAVES_W"]), int(cfg["WAVES_T"]), int(cfg.get("WAVES_K", 1)),
+                       int(cfg.get("K_UNROLL", 1)),
                        int(cfg["STAGES"]),
                        int(cfg.get("SPLIT", 1)), _split_mode(cfg, "none"),
                        int(cfg.get("GROUP_SIZE_M", 1)), _flags(cfg), k_fixed)
