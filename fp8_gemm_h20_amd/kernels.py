@@ -84,6 +84,8 @@ RING = (
     (64, 64, 4, 1, 4, 0, 2, 2), (64, 64, 4, 1, 8, 0, 2, 2),
     (64, 64, 4, 1, 8, 0, 4, 2), (64, 64, 4, 1, 8, 0, 4, 4),
     (128, 64, 4, 1, 6, 0, 2, 2), (128, 32, 4, 1, 4, 0, 2, 2),
+    # 8 waves on a 128x128 tile (two per SIMD): mid M with ~256 tiles
+    (128, 128, 4, 2, 2, 0, 1, 1), (128, 128, 4, 2, 3, 0, 1, 1), (128, 128, 4, 2, 4, 0, 2, 1),
 )
 # back-compat name used by tests and the tuner
 INSTANCES = TILED
