@@ -55,7 +55,9 @@ extern "C" {
 #define FP8BG_KIND_SKINNY 1
 /* LDS-ring kernel: like FP8BG_KIND_TILED, but each 128-K group is copied
  * global -> LDS by direct-to-LDS loads into a `stages`-deep ring (no register
- * staging, one barrier per group); 4 or 8 waves.  Requires M*K and N*K below
+ * staging, one barrier per `unroll` groups); waves_w x waves_t waves (4, 8
+ * or 12), times waves_k K slices that split the tile's 128-K groups and sum
+ * their partial tiles in fixed slice order.  Requires M*K and N*K below
  * 2^32. */
 #define FP8BG_KIND_RING   2
 
@@ -96,7 +98,9 @@ typedef struct fp8bg_config {
     int32_t block_t;    /* tokens (M) per workgroup tile */
     int32_t waves_w;    /* tiled/ring: waves along N inside the tile */
     int32_t waves_t;    /* tiled/ring: waves along M inside the tile */
-    int32_t waves_k;    /* skinny: waves splitting K inside a workgroup (4 or 8) */
+    int32_t waves_k;    /* skinny: waves splitting K inside a workgroup (4 or 8);
+                           ring: K slices of waves_w x waves_t waves (1, 2 or 4;
+                           0 means 1) */
     int32_t unroll;     /* skinny: 128-K groups in flight per wave;
                            ring: 128-K groups per barrier (1, 2 or 4; 0 means 1);
                            K/128/split must be a multiple of it */
