@@ -439,6 +439,11 @@ template <int R>
 struct WaveRole {
     static constexpr int value = R;
 };
+// whether a ring step issues the loads of the groups ST - KU ahead
+template <bool B>
+struct Loads {
+    static constexpr bool value = B;
+};
 
 // Workgroup tile TW weight rows x TT tokens, WW x WT waves.  Each 128-K group
 // of the stacked [weights; tokens] tile (TW + TT rows of 128 bytes) is copied
@@ -603,11 +608,13 @@ void fp8bg_ring(KArgs a) {
         return (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
 
-    // Every step issues its loads unconditionally so the vmcnt bookkeeping is
-    // the same in every iteration: group indices past the range are clamped
-    // to the last group (an L2 hit), and such a load lands in a stage that no
-    // later step reads (the stage of group g is read only by group g, and a
-    // clamped index g is past the last group).
+    // Every step but the last issues its loads unconditionally so the vmcnt
+    // bookkeeping is the same in every iteration: group indices past the
+    // range are clamped to the last group (an L2 hit), and such a load lands
+    // in a stage that no later step reads (the stage of group g is read only
+    // by group g, and a clamped index g is past the last group).  The last
+    // step's loads would all be clamped; it is peeled off without them (no
+    // wait counts the loads issued after the ones it waits for).
     const int g_last = k_lo + kcount - 1;
     for (int s = ks; s < ST - KU; s += WK) dma(min(k_lo + s, g_last), s);
 
@@ -625,8 +632,9 @@ void fp8bg_ring(KArgs a) {
     // and the older one for the rest (about 2% faster; no effect on smaller
     // tiles, so they keep one role).
     constexpr bool kPrio = WT == 2 && TW * TT >= 256 * 256;
-    auto group = [&](int i, int g_next, int s_next, auto role) {
+    auto group = [&](int i, int g_next, int s_next, auto role, auto load) {
         constexpr int R = decltype(role)::value;
+        constexpr bool LD = decltype(load)::value;
         const unsigned char* st = lds + (i % ST) * STAGE;
         const float* sc = (const float*)(st + OPS);
         // The group's first operands are read in the order the first token
@@ -664,8 +672,8 @@ void fp8bg_ring(KArgs a) {
             }
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
-                if ((j * NT) / (2 * NJ) == t) dma_block(j, g_next, s_next);
-            if (t == NT / 2) dma_scales(g_next, s_next);
+                if (LD && (j * NT) / (2 * NJ) == t) dma_block(j, g_next, s_next);
+            if (LD && t == NT / 2) dma_scales(g_next, s_next);
             if (kPrio && t == 0) {
                 if (R) __builtin_amdgcn_s_setprio(1);
                 else __builtin_amdgcn_s_setprio(0);
@@ -697,9 +705,9 @@ void fp8bg_ring(KArgs a) {
         for (int w = 0; w < NW; ++w) promote(acc[w][NT - 1], prev[w], s_prev);
     };
 
-    auto main_loop = [&](auto role) {
-#pragma unroll (KF ? KF / KU : 1)
-    for (int i = 0; i < kcount; i += KU) {
+    // One barrier step: groups i .. i + KU - 1, with (load) or without the
+    // loads of groups i + ST - KU .. i + ST - 1.
+    auto step = [&](int i, auto role, auto load) {
         // Groups i .. i + KU - 1 are complete once at most the DMA
         // instructions of the ST - 2 KU later groups are outstanding (vmcnt
         // retires in issue order; a wave loads only its slice's groups, 1 in
@@ -719,9 +727,15 @@ void fp8bg_ring(KArgs a) {
             // both belong to this wave's slice
             const int u = uk * WK + ks;
             const int g = i + ST - KU + u;
-            group(i + u, min(k_lo + g, g_last), g % ST, role);
+            group(i + u, min(k_lo + g, g_last), g % ST, role, load);
         }
-    }
+    };
+    // The last step is peeled off outside the loop (a second copy inside the
+    // loop body would make the large tiles spill).
+    auto main_loop = [&](auto role) {
+#pragma unroll (KF ? KF / KU - 1 : 1)
+        for (int i = 0; i + KU < kcount; i += KU) step(i, role, Loads<true>{});
+        step(kcount - KU, role, Loads<false>{});
     };
     // a uniform branch around two copies of the loop, so the priority
     // switches are immediates inside straight-line code
@@ -731,7 +745,7 @@ void fp8bg_ring(KArgs a) {
         main_loop(WaveRole<0>{});
     }
     if (kPrio) __builtin_amdgcn_s_setprio(0);
-    // The clamped loads of the last ST - KU groups are still in flight: they
+    // The clamped loads of the last ST - 2 KU groups are still in flight: they
     // must land before the LDS is reused below or handed to another workgroup.
     wait_vmcnt<0>();
 
