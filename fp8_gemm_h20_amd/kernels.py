@@ -86,6 +86,10 @@ RING = (
     (128, 64, 4, 1, 6, 0, 2, 2), (128, 32, 4, 1, 4, 0, 2, 2),
     # 8 waves on a 128x128 tile (two per SIMD): mid M with ~256 tiles
     (128, 128, 4, 2, 2, 0, 1, 1), (128, 128, 4, 2, 3, 0, 1, 1), (128, 128, 4, 2, 4, 0, 2, 1),
+    # token tiles that are not powers of two, for M that they cover with
+    # little waste (M=777 in 5 tiles of 160: 97% of the rows used)
+    (256, 160, 4, 2, 2, 0, 1, 1), (256, 192, 4, 2, 2, 0, 1, 1),
+    (128, 160, 2, 2, 3, 0, 1, 1), (128, 96, 2, 2, 4, 0, 1, 1),
 )
 # back-compat name used by tests and the tuner
 INSTANCES = TILED
