@@ -11,7 +11,7 @@ from pathlib import Path
 
 LIB_NAME = "libfp8bg.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK = 0
 ERR_SHAPE = 1
@@ -45,6 +45,8 @@ EXPORTS = (
     "fp8bg_gemm_bf16a",
     "fp8bg_quant_act",
     "fp8bg_e4m3_encode_host",
+    "fp8bg_calib_mfma",
+    "fp8bg_calib_read",
     "fp8bg_strerror",
 )
 
@@ -134,6 +136,10 @@ def _declare(lib):
     lib.fp8bg_quant_act.restype = ctypes.c_int
     lib.fp8bg_e4m3_encode_host.argtypes = [vp, vp, i64]
     lib.fp8bg_e4m3_encode_host.restype = ctypes.c_int
+    lib.fp8bg_calib_mfma.argtypes = [vp, vp, i32, i32, vp]
+    lib.fp8bg_calib_mfma.restype = ctypes.c_int
+    lib.fp8bg_calib_read.argtypes = [vp, i64, vp, i32, vp]
+    lib.fp8bg_calib_read.restype = ctypes.c_int
     lib.fp8bg_strerror.argtypes = [ctypes.c_int]
     lib.fp8bg_strerror.restype = ctypes.c_char_p
 

@@ -1299,6 +1299,61 @@ int find_instance(const fp8bg_config* c) {
 
 }  // namespace
 
+// ===========================================================================
+// Calibration kernels (measurement only): the MFMA issue rate and the
+// streaming-read rate this chip sustains, next to the published peaks.
+// ===========================================================================
+constexpr int kCalibMfmaPerIter = 16;
+
+// Each wave issues kCalibMfmaPerIter FP8 16x16x128 MFMAs per iteration from
+// register operands into 4 independent accumulators (so no MFMA waits for
+// the previous one's result).  The empty asm statements make the operands
+// opaque each iteration, so nothing is hoisted or folded.  With every code
+// 0x38 (1.0) each output element of an accumulator grows by 128 per MFMA:
+// out = 4 * 128 * (kCalibMfmaPerIter / 4) * iters, exact in fp32 for the
+// iteration counts the entry point accepts.
+__global__ __launch_bounds__(256) void fp8bg_calib_mfma_kernel(const int32_t* codes, float* out,
+                                                               int iters) {
+    const int lane = threadIdx.x & 63;
+    i32x8 a[2], b[2];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        a[0][e] = codes[(0 * 8 + e) * 64 + lane];
+        a[1][e] = codes[(1 * 8 + e) * 64 + lane];
+        b[0][e] = codes[(2 * 8 + e) * 64 + lane];
+        b[1][e] = codes[(3 * 8 + e) * 64 + lane];
+    }
+    f32x4 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < iters; ++it) {
+        asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]));
+#pragma unroll
+        for (int u = 0; u < kCalibMfmaPerIter; ++u)
+            acc[u & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                a[u & 1], b[(u >> 1) & 1], acc[u & 3], 0, 0, 0, 0, 0, 0);
+    }
+    out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc[0][0] + acc[1][0] + acc[2][0] + acc[3][0];
+}
+
+// Grid-stride read of n16 16-byte words, four loads in flight per lane,
+// XOR-folded; one 32-bit word per thread is written.
+__global__ __launch_bounds__(256) void fp8bg_calib_read_kernel(const i32x4* src, int64_t n16,
+                                                               uint32_t* out) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    i32x4 x = {0, 0, 0, 0};
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const i32x4 v0 = src[i];
+        const i32x4 v1 = src[i + stride];
+        const i32x4 v2 = src[i + 2 * stride];
+        const i32x4 v3 = src[i + 3 * stride];
+        x ^= v0 ^ v1 ^ v2 ^ v3;
+    }
+    for (; i < n16; i += stride) x ^= src[i];
+    out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = (uint32_t)(x[0] ^ x[1] ^ x[2] ^ x[3]);
+}
+
 extern "C" {
 
 int fp8bg_version(void) { return FP8BG_ABI_VERSION; }
@@ -1530,6 +1585,26 @@ int fp8bg_quant_act(const void* x, int64_t x_stride_m, void* q, float* s, int64_
     a.eps = eps;
     hipLaunchKernelGGL(fp8bg_quant_act_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
                        (hipStream_t)stream, a);
+    return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
+}
+
+int fp8bg_calib_mfma(const int32_t* codes, float* out, int32_t workgroups, int32_t iters,
+                     void* stream) {
+    if (!codes || !out) return FP8BG_ERR_NULL;
+    if (workgroups < 1 || iters < 1 || iters > FP8BG_CALIB_MAX_ITERS) return FP8BG_ERR_SHAPE;
+    if ((((uintptr_t)codes) & 3) || (((uintptr_t)out) & 3)) return FP8BG_ERR_ALIGN;
+    hipLaunchKernelGGL(fp8bg_calib_mfma_kernel, dim3((unsigned)workgroups), dim3(256), 0,
+                       (hipStream_t)stream, (const int32_t*)codes, out, iters);
+    return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
+}
+
+int fp8bg_calib_read(const void* src, int64_t bytes, uint32_t* out, int32_t workgroups,
+                     void* stream) {
+    if (!src || !out) return FP8BG_ERR_NULL;
+    if (bytes < 16 || bytes % 16 || workgroups < 1) return FP8BG_ERR_SHAPE;
+    if ((((uintptr_t)src) & 15) || (((uintptr_t)out) & 3)) return FP8BG_ERR_ALIGN;
+    hipLaunchKernelGGL(fp8bg_calib_read_kernel, dim3((unsigned)workgroups), dim3(256), 0,
+                       (hipStream_t)stream, (const i32x4*)src, bytes / 16, out);
     return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
 }
 

@@ -40,7 +40,7 @@ extern "C" {
 
 /* ABI version returned by fp8bg_version(); bumped on any signature or struct
  * change. */
-#define FP8BG_ABI_VERSION 4
+#define FP8BG_ABI_VERSION 5
 
 /* ---- kernel kinds --------------------------------------------------------- */
 /* LDS-tiled kernel: a block_w x block_t workgroup tile, 4 waves in a
@@ -231,6 +231,28 @@ int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps,
  * No reference counterpart (the reference relies on torch's cast).
  */
 int fp8bg_e4m3_encode_host(const float* x, uint8_t* out, int64_t n);
+
+/*
+ * Calibration kernels: what this chip sustains, measured next to the
+ * published peaks (no reference counterpart; the measurement plan for this
+ * path asks for an MFMA-only and a streaming-read calibration).
+ *
+ * fp8bg_calib_mfma: `workgroups` workgroups of 256 threads (4 waves); each
+ * wave issues 16 FP8 16x16x128 MFMAs per iteration (65536 flops each), for
+ * `iters` iterations (1 .. FP8BG_CALIB_MAX_ITERS).  codes: 32 x 64 int32
+ * e4m3 operand words (word e of lane l at [e * 64 + l]); out: workgroups *
+ * 256 floats.  With every code byte 0x38 (1.0) each out value is
+ * 2048 * iters exactly.
+ *
+ * fp8bg_calib_read: reads `bytes` (a multiple of 16, src 16-byte aligned)
+ * with `workgroups` workgroups of 256 threads and writes workgroups * 256
+ * uint32 words whose XOR equals the XOR of all 32-bit words of src.
+ */
+#define FP8BG_CALIB_MAX_ITERS 8192
+int fp8bg_calib_mfma(const int32_t* codes, float* out, int32_t workgroups, int32_t iters,
+                     void* stream);
+int fp8bg_calib_read(const void* src, int64_t bytes, uint32_t* out, int32_t workgroups,
+                     void* stream);
 
 /* Static message for an error code. */
 const char* fp8bg_strerror(int code);
