@@ -1195,7 +1195,8 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(128, 32, 4, 1, 4, 0, 2, 2) X(128, 128, 4, 2, 2, 0, 1, 1)   \
     X(128, 128, 4, 2, 3, 0, 1, 1) X(128, 128, 4, 2, 4, 0, 2, 1) \
     X(256, 160, 4, 2, 2, 0, 1, 1) X(256, 192, 4, 2, 2, 0, 1, 1)   \
-    X(128, 160, 2, 2, 3, 0, 1, 1) X(128, 96, 2, 2, 4, 0, 1, 1)
+    X(128, 160, 2, 2, 3, 0, 1, 1) X(128, 96, 2, 2, 4, 0, 1, 1)    \
+    X(64, 64, 2, 2, 8, 0, 4, 1)
 
 // skinny with the fused activation quantiser: the 16-token (NT = 1) tiles
 // (4, 1, 8, 4) left out: with the bf16 staging it needs more than 256 VGPRs

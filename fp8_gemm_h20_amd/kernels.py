@@ -90,6 +90,8 @@ RING = (
     # little waste (M=777 in 5 tiles of 160: 97% of the rows used)
     (256, 160, 4, 2, 2, 0, 1, 1), (256, 192, 4, 2, 2, 0, 1, 1),
     (128, 160, 2, 2, 3, 0, 1, 1), (128, 96, 2, 2, 4, 0, 1, 1),
+    # 64x64 with 2x2 waves (two weight blocks per wave)
+    (64, 64, 2, 2, 8, 0, 4, 1),
 )
 # back-compat name used by tests and the tuner
 INSTANCES = TILED
