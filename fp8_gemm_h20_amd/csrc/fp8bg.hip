@@ -705,6 +705,59 @@ void fp8bg_ring(KArgs a) {
         for (int w = 0; w < NW; ++w) promote(acc[w][NT - 1], prev[w], s_prev);
     };
 
+    // Tiles with a 2-stage ring and one group per barrier write C from the
+    // last group itself (tiles without a K split): its step issues no loads,
+    // so the other stage is idle, and token block t's C rows are final once
+    // its products are promoted.  Each wave stages them in its own slice of
+    // the idle stage (16 rows, double-buffered) and stores them while the
+    // MFMAs of the later blocks run, instead of after a barrier at the end:
+    // 1-7% faster on the large tiles, bitwise the same output.  The products
+    // are promoted right after their own MFMAs here (no second set of product
+    // registers), which keeps the 256x256 tile's registers within bounds.
+    constexpr bool kEarlyC = ST == 2 && KU == 1 && WK == 1 && KF == 0;
+    static_assert(!kEarlyC || NWAVE * 2 * 16 * ROWB <= STAGE, "C staging inside the idle stage");
+    auto group_last = [&](int i) __attribute__((always_inline)) {
+        const unsigned char* st = lds + (i % ST) * STAGE;
+        const float* sc = (const float*)(st + OPS);
+        unsigned char* creg = lds + ((i + 1) % ST) * STAGE + wave * (2 * 16 * ROWB);
+        const uint16_t* bl = (const uint16_t*)(st + OPS + (TT + NBS) * 4);
+        i32x8 top = opread(st, TW + wv_t * WTT + (lane & 15));
+        i32x8 wop[NW];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) wop[w] = opread(st, wv_w * WTW + w * 16 + (lane & 15));
+        const float sb = sc[TT + (w0 % 128 + wv_w * WTW) / 128];
+        const int r = lane & 15, qd = lane >> 4;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float s_t = sc[wv_t * WTT + t * 16 + (lane & 15)] * sb;
+            i32x8 top_next = top;
+            if (t + 1 < NT) top_next = opread(st, TW + wv_t * WTT + (t + 1) * 16 + (lane & 15));
+#pragma unroll
+            for (int w = 0; w < NW; ++w) promote(acc[w][t], mfma16x16x128(wop[w], top), s_t);
+            top = top_next;
+            // rows of token block t: chunk c of row r at slot c ^ (r % CPR)
+            int mb = t0 + wv_t * WTT + t * 16;
+            asm volatile("" : "+v"(mb));          // computed here, not hoisted
+            unsigned char* reg = creg + (t & 1) * (16 * ROWB);
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+                *(uint2*)(reg + r * ROWB + (((2 * w + (qd >> 1)) ^ (r % CPR)) << 4) + (qd & 1) * 8) =
+                    a.bias ? out_bf16x4v(acc[w][t], true,
+                                         *(const uint2*)(bl + wv_w * WTW + w * 16 + qd * 4))
+                           : pack_bf16x4(acc[w][t]);
+#pragma unroll
+            for (int h = 0; h < (16 * CPR + 63) / 64; ++h) {
+                const int idx = lane + 64 * h;
+                const int row = idx / CPR, c = idx % CPR;
+                if (row >= 16) continue;
+                const i32x4 v = *(const i32x4*)(reg + row * ROWB + ((c ^ (row % CPR)) << 4));
+                const int m = mb + row, n = w0 + wv_w * WTW + c * 8;
+                if (m < a.M && n < a.N)
+                    __builtin_nontemporal_store(v, (i32x4*)(a.C + (size_t)m * a.N + n));
+            }
+        }
+    };
+
     // One barrier step: groups i .. i + KU - 1, with (load) or without the
     // loads of groups i + ST - KU .. i + ST - 1.
     auto step = [&](int i, auto role, auto load) {
@@ -732,17 +785,45 @@ void fp8bg_ring(KArgs a) {
     };
     // The last step is peeled off outside the loop (a second copy inside the
     // loop body would make the large tiles spill).
-    auto main_loop = [&](auto role) {
-#pragma unroll (KF ? KF / KU - 1 : 1)
-        for (int i = 0; i + KU < kcount; i += KU) step(i, role, Loads<true>{});
-        step(kcount - KU, role, Loads<false>{});
-    };
     // a uniform branch around two copies of the loop, so the priority
     // switches are immediates inside straight-line code
-    if (kPrio && wv_t) {
-        main_loop(WaveRole<1>{});
+    if constexpr (kEarlyC) {
+        // the last step is dispatched after the loop, and the C-writing one
+        // returns right away (a path that rejoined the epilogue would keep
+        // the epilogue's registers alive through it)
+        auto main_loop = [&](auto role) {
+            for (int i = 0; i + KU < kcount; i += KU) step(i, role, Loads<true>{});
+        };
+        if (kPrio && wv_t) {
+            main_loop(WaveRole<1>{});
+        } else {
+            main_loop(WaveRole<0>{});
+        }
+        if (blockIdx.x < a.n_dp) {
+            wait_vmcnt_lds<0>();
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (kPrio) __builtin_amdgcn_s_setprio(0);
+            group_last(kcount - 1);
+            return;
+        }
+        if (kPrio && wv_t) {
+            step(kcount - KU, WaveRole<1>{}, Loads<false>{});
+        } else {
+            step(kcount - KU, WaveRole<0>{}, Loads<false>{});
+        }
     } else {
-        main_loop(WaveRole<0>{});
+        auto main_loop = [&](auto role) {
+#pragma unroll (KF ? KF / KU - 1 : 1)
+            for (int i = 0; i + KU < kcount; i += KU) step(i, role, Loads<true>{});
+            step(kcount - KU, role, Loads<false>{});
+        };
+        if (kPrio && wv_t) {
+            main_loop(WaveRole<1>{});
+        } else {
+            main_loop(WaveRole<0>{});
+        }
     }
     if (kPrio) __builtin_amdgcn_s_setprio(0);
     // The clamped loads of the last ST - 2 KU groups are still in flight: they
