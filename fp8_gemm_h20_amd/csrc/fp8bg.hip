@@ -705,21 +705,24 @@ void fp8bg_ring(KArgs a) {
         for (int w = 0; w < NW; ++w) promote(acc[w][NT - 1], prev[w], s_prev);
     };
 
-    // Tiles with a 2-stage ring and one group per barrier write C from the
-    // last group itself (tiles without a K split): its step issues no loads,
-    // so the other stage is idle, and token block t's C rows are final once
-    // its products are promoted.  Each wave stages them in its own slice of
-    // the idle stage (16 rows, double-buffered) and stores them while the
-    // MFMAs of the later blocks run, instead of after a barrier at the end:
-    // 1-7% faster on the large tiles, bitwise the same output.  The products
+    // Tiles with one group per barrier write C from the last group itself
+    // (tiles without a K split): its step issues no loads, so the stage of
+    // the group before (read by every wave before the barrier, and the
+    // target of no later load) is idle, and token block t's C rows are
+    // final once its products are promoted.  Each wave stages them in its
+    // own 16-row slice of the idle stage (reused block after block: a wave's
+    // LDS operations run in order) and stores them while the MFMAs of the
+    // later blocks run, instead of after a barrier at the end:
+    // 1-7% faster on tiles from 128x128 up (smaller ones, whose epilogue is
+    // short, do not gain), bitwise the same output.  The products
     // are promoted right after their own MFMAs here (no second set of product
     // registers), which keeps the 256x256 tile's registers within bounds.
-    constexpr bool kEarlyC = ST == 2 && KU == 1 && WK == 1 && KF == 0;
-    static_assert(!kEarlyC || NWAVE * 2 * 16 * ROWB <= STAGE, "C staging inside the idle stage");
+    constexpr bool kEarlyC = KU == 1 && WK == 1 && KF == 0 && TW * TT >= 128 * 128;
+    static_assert(!kEarlyC || NWAVE * 16 * ROWB <= STAGE, "C staging inside the idle stage");
     auto group_last = [&](int i) __attribute__((always_inline)) {
         const unsigned char* st = lds + (i % ST) * STAGE;
         const float* sc = (const float*)(st + OPS);
-        unsigned char* creg = lds + ((i + 1) % ST) * STAGE + wave * (2 * 16 * ROWB);
+        unsigned char* reg = lds + ((i + ST - 1) % ST) * STAGE + wave * (16 * ROWB);
         const uint16_t* bl = (const uint16_t*)(st + OPS + (TT + NBS) * 4);
         i32x8 top = opread(st, TW + wv_t * WTT + (lane & 15));
         i32x8 wop[NW];
@@ -738,7 +741,6 @@ void fp8bg_ring(KArgs a) {
             // rows of token block t: chunk c of row r at slot c ^ (r % CPR)
             int mb = t0 + wv_t * WTT + t * 16;
             asm volatile("" : "+v"(mb));          // computed here, not hoisted
-            unsigned char* reg = creg + (t & 1) * (16 * ROWB);
 #pragma unroll
             for (int w = 0; w < NW; ++w)
                 *(uint2*)(reg + r * ROWB + (((2 * w + (qd >> 1)) ^ (r % CPR)) << 4) + (qd & 1) * 8) =
@@ -800,6 +802,8 @@ void fp8bg_ring(KArgs a) {
             main_loop(WaveRole<0>{});
         }
         if (blockIdx.x < a.n_dp) {
+            // vmcnt(0): the clamped loads of deeper rings land here, so none
+            // writes the LDS after this workgroup has returned
             wait_vmcnt_lds<0>();
             asm volatile("" ::: "memory");
             __builtin_amdgcn_s_barrier();
