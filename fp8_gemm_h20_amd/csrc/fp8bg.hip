@@ -713,11 +713,13 @@ void fp8bg_ring(KArgs a) {
     // own 16-row slice of the idle stage (reused block after block: a wave's
     // LDS operations run in order) and stores them while the MFMAs of the
     // later blocks run, instead of after a barrier at the end:
-    // 1-7% faster on tiles from 128x128 up (smaller ones, whose epilogue is
-    // short, do not gain), bitwise the same output.  The products
+    // 2-5% faster on tiles from 128x128 up (smaller ones, whose epilogue is
+    // short, do not gain), bitwise the same output.  Not on the 256x256
+    // tile: there it wrote 19% more bytes to HBM (WRITE_SIZE) and ran 2%
+    // slower, while every other tile's writes stayed at C's size.  The products
     // are promoted right after their own MFMAs here (no second set of product
-    // registers), which keeps the 256x256 tile's registers within bounds.
-    constexpr bool kEarlyC = KU == 1 && WK == 1 && KF == 0 && TW * TT >= 128 * 128;
+    // registers).
+    constexpr bool kEarlyC = KU == 1 && WK == 1 && KF == 0 && TW * TT >= 128 * 128 && !kPrio;
     static_assert(!kEarlyC || NWAVE * 16 * ROWB <= STAGE, "C staging inside the idle stage");
     auto group_last = [&](int i) __attribute__((always_inline)) {
         const unsigned char* st = lds + (i % ST) * STAGE;
