@@ -469,10 +469,16 @@ struct Loads {
 // tiles are summed through LDS in fixed slice order at the end: for tiles
 // with few workgroups and long K (narrow N at small M), WK times the loads
 // and MFMAs in flight without a second launch.
-template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK>
-__global__ __launch_bounds__(64 * WW * WT * WK)
-__attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
-void fp8bg_ring(KArgs a) {
+// Whether a ring instance also has an fp8bg_ring_dp kernel: the instances
+// whose last group can write C itself (see group_last below).
+constexpr bool ring_has_dp(int TW, int TT, int KF, int KU, int WK) {
+    return KU == 1 && WK == 1 && KF == 0 && TW * TT >= 128 * 128;
+}
+
+// The ring kernel's body.  DPO: every workgroup of the launch is a whole
+// (data-parallel) tile, none computes a K split.
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK, bool DPO>
+__device__ __forceinline__ void ring_body(const KArgs& a) {
     constexpr int NWAVE = WW * WT;                // waves of one K slice
     constexpr int WTW = TW / WW;
     constexpr int WTT = TT / WT;
@@ -713,13 +719,13 @@ void fp8bg_ring(KArgs a) {
     // own 16-row slice of the idle stage (reused block after block: a wave's
     // LDS operations run in order) and stores them while the MFMAs of the
     // later blocks run, instead of after a barrier at the end:
-    // 2-5% faster on tiles from 128x128 up (smaller ones, whose epilogue is
-    // short, do not gain), bitwise the same output.  Not on the 256x256
-    // tile: there it wrote 19% more bytes to HBM (WRITE_SIZE) and ran 2%
-    // slower, while every other tile's writes stayed at C's size.  The products
+    // 1-5% faster on tiles from 128x128 up (smaller ones, whose epilogue is
+    // short, do not gain), bitwise the same output.  The 256x256 tile takes
+    // this path only in fp8bg_ring_dp: beside the split tiles' epilogue its
+    // registers spill at the end of the loop.  The products
     // are promoted right after their own MFMAs here (no second set of product
     // registers).
-    constexpr bool kEarlyC = KU == 1 && WK == 1 && KF == 0 && TW * TT >= 128 * 128 && !kPrio;
+    constexpr bool kEarlyC = ring_has_dp(TW, TT, KF, KU, WK) && (DPO || !kPrio);
     static_assert(!kEarlyC || NWAVE * 16 * ROWB <= STAGE, "C staging inside the idle stage");
     auto group_last = [&](int i) __attribute__((always_inline)) {
         const unsigned char* st = lds + (i % ST) * STAGE;
@@ -803,7 +809,7 @@ void fp8bg_ring(KArgs a) {
         } else {
             main_loop(WaveRole<0>{});
         }
-        if (blockIdx.x < a.n_dp) {
+        if (DPO || blockIdx.x < a.n_dp) {
             // vmcnt(0): the clamped loads of deeper rings land here, so none
             // writes the LDS after this workgroup has returned
             wait_vmcnt_lds<0>();
@@ -938,6 +944,23 @@ void fp8bg_ring(KArgs a) {
             *(f32x4*)(mine + tl * TW + wl) = acc[w][t];
         }
     }
+}
+
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK>
+__global__ __launch_bounds__(64 * WW * WT * WK)
+__attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
+void fp8bg_ring(KArgs a) {
+    ring_body<TW, TT, WW, WT, ST, KF, KU, WK, false>(a);
+}
+
+// The same for launches without split tiles: with no epilogue path left
+// beside the last group's C writes, the 256x256 tile takes them too (in the
+// kernel above its registers would spill at the loop's end).
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK>
+__global__ __launch_bounds__(64 * WW * WT * WK)
+__attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
+void fp8bg_ring_dp(KArgs a) {
+    ring_body<TW, TT, WW, WT, ST, KF, KU, WK, true>(a);
 }
 
 // ===========================================================================
@@ -1324,6 +1347,13 @@ FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_LAUNCHER)
 #define FP8BG_RING_LAUNCHER(TW, TT, WW, WT, ST, KF, KU, WK)                                  \
     static void ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF##_##KU##_##WK(                   \
         dim3 g, size_t shm, hipStream_t s, const KArgs& a) {                                  \
+        if constexpr (ring_has_dp(TW, TT, KF, KU, WK)) {                                      \
+            if (a.n_dp == (int)g.x) {                                                         \
+                hipLaunchKernelGGL((fp8bg_ring_dp<TW, TT, WW, WT, ST, KF, KU, WK>), g,       \
+                                   dim3(64 * WW * WT * WK), shm, s, a);                       \
+                return;                                                                       \
+            }                                                                                 \
+        }                                                                                     \
         hipLaunchKernelGGL((fp8bg_ring<TW, TT, WW, WT, ST, KF, KU, WK>), g,                  \
                            dim3(64 * WW * WT * WK), shm, s, a);                               \
     }
