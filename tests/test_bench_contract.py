@@ -19,7 +19,7 @@ def test_more_than_one_gpu_exits_with_a_message():
 
 
 def test_algorithmic_counts():
-    # SURVEY-defined units: flops 2MNK; bytes A + B + As + Bs + C (bf16)
+    # algorithmic units: flops 2MNK; bytes A + B + As + Bs + C (bf16)
     m, n, k = 200, 3072, 2048
     assert bench.flops(m, n, k) == 2 * m * n * k
     assert bench.algo_bytes(m, n, k) == m * k + n * k + 4 * m * (k // 128) + 4 * (n // 128) * (k // 128) + 2 * m * n
