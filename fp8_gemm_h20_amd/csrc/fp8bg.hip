@@ -889,19 +889,25 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
                         acc[w][t][3] += v[3];
                     }
         }
+        if (ks > 0) return;
     }
+    // with K slices, slice 0 stages C after the parked partial tiles, so it
+    // needs no barrier between adding them and writing C
+    constexpr int kCOff = (WK - 1) * TW * TT * 4;
+    static_assert(kCOff + NWAVE * WTT * ROWB <= ST * STAGE, "C staging after the partial tiles");
     if (dp) {
         // bf16 C through LDS: once every wave has passed the barrier below the
         // whole ring is free, and each wave of slice 0 writes its WTT x WTW
         // tile into its own region (row-major, chunk c of row r at slot
         // c ^ (r % CPR)), reads it back as whole 16-byte chunks and stores
         // full 128-byte lines with non-temporal stores (C is not re-read).
-        wait_vmcnt_lds<0>();
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        if (ks > 0) return;
-        unsigned char* region = lds + wave * (WTT * ROWB);
+        if (WK == 1) {
+            wait_vmcnt_lds<0>();
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        }
+        unsigned char* region = lds + kCOff + wave * (WTT * ROWB);
         auto stage_c = [&](auto pack) {
 #pragma unroll
             for (int t = 0; t < NT; ++t)
