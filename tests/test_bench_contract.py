@@ -44,3 +44,24 @@ def test_workload_grids_are_covered_by_their_profiles(workload):
     for n, k in nks:
         for m in ms:
             assert supports(workload, m, n, k), (workload, m, n, k)
+
+
+def test_kernel_names_follow_the_built_kernels():
+    # bench.kernel_name names fp8bg_ring_dp for unsplit ring entries exactly
+    # where the library builds one (the launcher then runs it)
+    import re
+    import shutil
+    import subprocess
+    from fp8_gemm_h20_amd import _lib, kernels
+    if shutil.which("nm") is None or not _lib.LIB_PATH.exists():
+        pytest.skip("nm or the built library is not available")
+    syms = subprocess.run(["nm", "-C", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
+    built = {tuple(int(v) for v in m.split(", "))
+             for m in re.findall(r"fp8bg_ring_dp<([0-9, ]+)>\(", syms)}
+    named = set()
+    for tw, tt, ww, wt, st, kf, ku, wk in kernels.RING:
+        cfg = dict(BLOCK_W=tw, BLOCK_T=tt, WAVES_W=ww, WAVES_T=wt, STAGES=st, K_FIXED=kf,
+                   K_UNROLL=ku, WAVES_K=wk)
+        if bench.kernel_name({"impl": "ring", "config": cfg}).startswith("fp8bg_ring_dp<"):
+            named.add((tw, tt, ww, wt, st, kf, ku, wk))
+    assert built and built == named
