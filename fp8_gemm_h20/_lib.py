@@ -154,9 +154,9 @@ def lib():
             path = os.environ.get("FP8BG_LIB", str(LIB_PATH))
             if not os.path.exists(path):
                 raise RuntimeError(
-                    f"fp8_gemm_h20_amd: HIP library {path} is not built; run "
+                    f"fp8_gemm_h20: HIP library {path} is not built; run "
                     "`python -c 'import __graft_entry__ as g; g.build()'` or "
-                    "`python -m fp8_gemm_h20_amd.build` first")
+                    "`python -m fp8_gemm_h20.build` first")
             handle = ctypes.CDLL(path)
             _declare(handle)
             ver = handle.fp8bg_version()

@@ -1,4 +1,4 @@
-"""Build libfp8bg.so in-tree: `python -m fp8_gemm_h20_amd.build`.
+"""Build libfp8bg.so in-tree: `python -m fp8_gemm_h20.build`.
 
 hipcc cross-compiles for gfx950 without a GPU.  Packed-fp32 VALU forms are
 disabled for all device code (-packed-fp32-ops), and MFMA instructions use the

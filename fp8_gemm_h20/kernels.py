@@ -93,9 +93,6 @@ RING = (
     # 64x64 with 2x2 waves (two weight blocks per wave)
     (64, 64, 2, 2, 8, 0, 4, 1),
 )
-# back-compat name used by tests and the tuner
-INSTANCES = TILED
-
 SPLIT_MODES = {"none": _lib.SPLIT_NONE, "tail": _lib.SPLIT_TAIL, "full": _lib.SPLIT_FULL}
 
 
@@ -180,9 +177,6 @@ def ring_struct(cfg, k_fixed=0):
                        int(cfg.get("SPLIT", 1)), _split_mode(cfg, "none"),
                        int(cfg.get("GROUP_SIZE_M", 1)), _flags(cfg), k_fixed)
 
-
-# back-compat alias
-native_struct = tiled_struct
 
 
 # ---------------------------------------------------------------------------
@@ -401,9 +395,6 @@ def shortk(A, B, As, Bs, config, **epilogue):
         config = {"BLOCK_W": tw, "BLOCK_T": tt, "GROUP_SIZE_M": int(config.get("GROUP", 1))}
     return launch(A, B, As, Bs, _tiled_cached(_freeze(config), 2), **epilogue)
 
-
-# earlier name of the tiled impl
-xdl = tiled
 
 
 # ---------------------------------------------------------------------------

@@ -15,7 +15,7 @@ Environment (the reference's names, so existing launch scripts keep working):
   FP8MM_HOME=/path        prepended to sys.path (where this package lives)
 
 Loading it into every SGLang process: put a `sitecustomize.py` containing
-`import fp8_gemm_h20_amd.sglang_patch` on PYTHONPATH (the reference's
+`import fp8_gemm_h20.sglang_patch` on PYTHONPATH (the reference's
 sgl_patch/sitecustomize.py does the same for its adapter), or import this
 module before SGLang builds its model.  Importing it does not import torch
 or load the HIP library; both wait for the first patched call.

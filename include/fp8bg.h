@@ -89,7 +89,7 @@ extern "C" {
 #define FP8BG_FLAG_SWZPAIR   0x8   /* swz = (r >> 1) & 7 */
 
 /*
- * Kernel configuration: one gfx950 table entry (fp8_gemm_h20_amd/configs/*.json).
+ * Kernel configuration: one gfx950 table entry (fp8_gemm_h20/configs/*.json).
  * Replaces the reference's per-entry `config` dict (fp8_gemm_h20/config.py:80-91).
  */
 typedef struct fp8bg_config {

@@ -2,7 +2,7 @@
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
 this package, and only as the checker (or the timed CPU baseline).  The
-product (fp8_gemm_h20_amd) never imports it and has no CPU fallback.
+product (fp8_gemm_h20) never imports it and has no CPU fallback.
 
 blockfp8.py restates, in numpy:
   * OCP e4m3 ("float8_e4m3fn") decode/encode and fp32 -> bf16 RNE rounding;

@@ -1,6 +1,6 @@
 """Regenerate the golden GEMM fixtures: `python tests/golden/make_golden.py`.
 
-Inputs come from the package's seeded recipe (fp8_gemm_h20_amd.quant.sample,
+Inputs come from the package's seeded recipe (fp8_gemm_h20.quant.sample,
 CPU torch.Generator) quantised by the oracle's numpy quantiser; expected
 outputs are the float64 dequant-matmul of the quantised operands (exact
 products, float64 sums), stored rounded to float32 plus the bf16 bits
@@ -18,7 +18,7 @@ HERE = Path(__file__).resolve().parent
 ROOT = HERE.parents[1]
 sys.path.insert(0, str(ROOT))
 
-from fp8_gemm_h20_amd import quant  # noqa: E402
+from fp8_gemm_h20 import quant  # noqa: E402
 from oracle import blockfp8 as ob  # noqa: E402
 
 CASES = [

@@ -39,7 +39,7 @@ def test_traffic_record_matches_the_packaged_table():
 
 @pytest.mark.parametrize("workload", sorted(bench.WORKLOADS))
 def test_workload_grids_are_covered_by_their_profiles(workload):
-    from fp8_gemm_h20_amd import supports
+    from fp8_gemm_h20 import supports
     nks, ms = bench.WORKLOADS[workload]
     for n, k in nks:
         for m in ms:
@@ -52,7 +52,7 @@ def test_kernel_names_follow_the_built_kernels():
     import re
     import shutil
     import subprocess
-    from fp8_gemm_h20_amd import _lib, kernels
+    from fp8_gemm_h20 import _lib, kernels
     if shutil.which("nm") is None or not _lib.LIB_PATH.exists():
         pytest.skip("nm or the built library is not available")
     syms = subprocess.run(["nm", "-C", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout

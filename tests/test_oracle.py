@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import blockfp8 as ob
-from fp8_gemm_h20_amd import quant
+from fp8_gemm_h20 import quant
 
 
 # ---------------------------------------------------------------- e4m3 / bf16
