@@ -255,3 +255,25 @@ def test_reciprocal_quantiser_differs_from_division_only_at_rounding_boundaries(
     q2, s2 = ob.quantize_act_reciprocal(row[None, :], eps=1e-10)
     assert s1[0, 0] == s2[0, 0] == np.float32(0.125)
     assert np.array_equal(q1, q2) and np.array_equal(q1[0, :127], np.arange(0, 127, dtype=np.uint8))
+
+
+def test_torch_cpu_baseline_matches_the_numpy_oracle():
+    # the bench's CPU baseline (torch restatement of validate.py:32-34 plus the
+    # bf16 cast) equals the numpy oracle up to fp32 summation order, and a
+    # transposed weight operand fails the same check
+    import torch
+    from fp8_gemm_h20 import quant
+    from oracle import torch_cpu
+    for m, n, k in [(1, 256, 128), (37, 384, 512), (200, 512, 1024)]:
+        A, B, As, Bs = quant.make_inputs(m, n, k, device="cpu")
+        got = torch_cpu.dequant_matmul_bf16(A, B, As, Bs)
+        assert got.dtype == torch.bfloat16 and got.shape == (m, n)
+        ref = ob.dequant_matmul(A.view(torch.uint8).numpy(), B.view(torch.uint8).numpy(),
+                                As.numpy(), Bs.numpy())
+        assert ob.error(got.float().numpy(), ref) <= 2 ** -8
+        assert ob.cosine(got.float().numpy(), ref) > 0.99999
+    A, B, As, Bs = quant.make_inputs(64, 256, 256, device="cpu")
+    bad = torch_cpu.dequant_matmul_bf16(A, B.view(2, 128, 2, 128).transpose(1, 3).reshape(256, 256)
+                                        .contiguous(), As, Bs)
+    ref = ob.dequant_matmul(A.view(torch.uint8).numpy(), B.view(torch.uint8).numpy(), As.numpy(), Bs.numpy())
+    assert ob.error(bad.float().numpy(), ref) > 0.1
