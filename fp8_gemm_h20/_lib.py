@@ -11,7 +11,7 @@ from pathlib import Path
 
 LIB_NAME = "libfp8bg.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 OK = 0
 ERR_SHAPE = 1
@@ -21,6 +21,10 @@ ERR_ALIGN = 4
 ERR_LAUNCH = 5
 ERR_DEVICE = 6
 ERR_NULL = 7
+ERR_SCRATCH = 8
+
+# fp32 elements of fp8bg_gemm_noalloc's static split-K scratch (FP8BG_SCRATCH_ELEMS)
+SCRATCH_ELEMS = 1 << 22
 
 KIND_TILED = 0
 KIND_SKINNY = 1
@@ -42,6 +46,7 @@ EXPORTS = (
     "fp8bg_make_plan",
     "fp8bg_config_supported",
     "fp8bg_gemm",
+    "fp8bg_gemm_noalloc",
     "fp8bg_gemm_bf16a",
     "fp8bg_quant_act",
     "fp8bg_e4m3_encode_host",
@@ -121,6 +126,8 @@ def _declare(lib):
         vp,                     # stream
     ]
     lib.fp8bg_gemm.restype = ctypes.c_int
+    lib.fp8bg_gemm_noalloc.argtypes = lib.fp8bg_gemm.argtypes[:15] + [vp]
+    lib.fp8bg_gemm_noalloc.restype = ctypes.c_int
     lib.fp8bg_gemm_bf16a.argtypes = [
         vp, i64, ctypes.c_float,  # X, row stride, eps
         vp, vp, i64, i64,       # B, Bs, strides

@@ -47,6 +47,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "fp8bg.h"
 
 namespace {
@@ -1492,6 +1495,8 @@ const char* fp8bg_strerror(int code) {
         case FP8BG_ERR_LAUNCH: return "HIP kernel launch failed";
         case FP8BG_ERR_DEVICE: return "HIP device query failed";
         case FP8BG_ERR_NULL: return "required pointer argument is NULL";
+        case FP8BG_ERR_SCRATCH:
+            return "split-K workspace larger than the library scratch (FP8BG_SCRATCH_ELEMS fp32)";
         default: return "unknown fp8bg error";
     }
 }
@@ -1573,19 +1578,30 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     return FP8BG_OK;
 }
 
-int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_m,
-               int64_t as_stride_k, const float* Bs, int64_t bs_stride_n, int64_t bs_stride_k,
-               const void* bias, void* C, int32_t M, int32_t N, int32_t K,
-               const fp8bg_config* cfg, int32_t num_cus, float* ws, int64_t ws_elems,
-               void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The GEMM enqueue shared by fp8bg_gemm (caller's workspace) and
+// fp8bg_gemm_noalloc (the library's static scratch): plan, checks, the GEMM
+// kernel and, for split tiles, the fixed-order reduction.  `ws_check`
+// validates the workspace size once the plan is known (it may refuse).
+template <typename WsCheck>
+int gemm_enqueue(const void* A, const void* B, const float* As, int64_t as_stride_m,
+                 int64_t as_stride_k, const float* Bs, int64_t bs_stride_n, int64_t bs_stride_k,
+                 const void* bias, void* C, int32_t M, int32_t N, int32_t K,
+                 const fp8bg_config* cfg, int32_t num_cus, void* stream, WsCheck ws_check) {
     if (!A || !B || !As || !Bs || !C) return FP8BG_ERR_NULL;
     if (((uintptr_t)bias) & 7) return FP8BG_ERR_ALIGN;
     fp8bg_plan p;
     const int rc = fp8bg_make_plan(M, N, K, cfg, num_cus, &p);
     if (rc != FP8BG_OK) return rc;
     if ((((uintptr_t)A) | ((uintptr_t)B) | ((uintptr_t)C)) & 15) return FP8BG_ERR_ALIGN;
-    if (p.n_split > 0 && (!ws || ws_elems < p.ws_elems || (((uintptr_t)ws) & 15)))
-        return FP8BG_ERR_WORKSPACE;
+    float* ws = nullptr;
+    if (p.n_split > 0) {
+        const int wrc = ws_check(p.ws_elems, &ws);
+        if (wrc != FP8BG_OK) return wrc;
+    }
 
     const Instance& k = kInstances[p.kernel_id];
     KArgs a = {};
@@ -1624,6 +1640,73 @@ int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_
         if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
     }
     return FP8BG_OK;
+}
+
+// Split-K scratch of fp8bg_gemm_noalloc: one copy per GPU, held until the
+// process ends.  In host code `scratch` names a host-side stand-in, not a
+// device address; kernels receive the per-device address that
+// hipGetSymbolAddress returns, looked up once per device with that device
+// current and kept in scratch_ptr.  No part of it needs to start at zero:
+// every split workgroup writes its whole fp32 slab before the reduction
+// kernel (later on the same stream) reads it.
+static __device__ __align__(256) float scratch[FP8BG_SCRATCH_ELEMS];
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> scratch_ptr[kMaxDevices];
+std::mutex scratch_mu;
+
+// Device address of `scratch` on the device of `stream` (which must be the
+// current device).
+int scratch_address(void* stream, float** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return FP8BG_ERR_DEVICE;
+    if (stream) {
+        hipDevice_t sdev = -1;
+        if (hipStreamGetDevice((hipStream_t)stream, &sdev) != hipSuccess || sdev != dev)
+            return FP8BG_ERR_DEVICE;
+    }
+    float* p = scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(scratch_mu);
+        p = scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            void* q = nullptr;
+            if (hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) != hipSuccess || !q) return FP8BG_ERR_DEVICE;
+            p = (float*)q;
+            scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return FP8BG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fp8bg_gemm(const void* A, const void* B, const float* As, int64_t as_stride_m,
+               int64_t as_stride_k, const float* Bs, int64_t bs_stride_n, int64_t bs_stride_k,
+               const void* bias, void* C, int32_t M, int32_t N, int32_t K,
+               const fp8bg_config* cfg, int32_t num_cus, float* ws, int64_t ws_elems,
+               void* stream) {
+    return gemm_enqueue(A, B, As, as_stride_m, as_stride_k, Bs, bs_stride_n, bs_stride_k, bias, C,
+                        M, N, K, cfg, num_cus, stream, [&](int64_t need, float** out) {
+                            if (!ws || ws_elems < need || (((uintptr_t)ws) & 15))
+                                return FP8BG_ERR_WORKSPACE;
+                            *out = ws;
+                            return FP8BG_OK;
+                        });
+}
+
+int fp8bg_gemm_noalloc(const void* A, const void* B, const float* As, int64_t as_stride_m,
+                       int64_t as_stride_k, const float* Bs, int64_t bs_stride_n,
+                       int64_t bs_stride_k, const void* bias, void* C, int32_t M, int32_t N,
+                       int32_t K, const fp8bg_config* cfg, int32_t num_cus, void* stream) {
+    return gemm_enqueue(A, B, As, as_stride_m, as_stride_k, Bs, bs_stride_n, bs_stride_k, bias, C,
+                        M, N, K, cfg, num_cus, stream, [&](int64_t need, float** out) {
+                            if (need > FP8BG_SCRATCH_ELEMS) return FP8BG_ERR_SCRATCH;
+                            return scratch_address(stream, out);
+                        });
 }
 
 int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps, const void* B, const float* Bs,

@@ -16,7 +16,9 @@
  * registered in fp8_gemm_h20/engine.py:5-19.  Each entry point below names the
  * reference interface it replaces.  All pointers are device pointers except
  * the config/plan structs and output scalars; no torch types cross this ABI.
- * Every function is reentrant; the library owns no device allocations.
+ * Every function is reentrant.  The library's only device memory is the
+ * static split-K scratch of fp8bg_gemm_noalloc (FP8BG_SCRATCH_ELEMS fp32 per
+ * GPU, part of the loaded code object, held until the process ends).
  */
 #ifndef FP8BG_H
 #define FP8BG_H
@@ -37,10 +39,11 @@ extern "C" {
 #define FP8BG_ERR_LAUNCH     5  /* hipLaunchKernel / hip runtime error */
 #define FP8BG_ERR_DEVICE     6  /* device query failed */
 #define FP8BG_ERR_NULL       7  /* required pointer argument is NULL */
+#define FP8BG_ERR_SCRATCH    8  /* split-K workspace beyond FP8BG_SCRATCH_ELEMS (fp8bg_gemm_noalloc) */
 
 /* ABI version returned by fp8bg_version(); bumped on any signature or struct
  * change. */
-#define FP8BG_ABI_VERSION 5
+#define FP8BG_ABI_VERSION 6
 
 /* ---- kernel kinds --------------------------------------------------------- */
 /* LDS-tiled kernel: a block_w x block_t workgroup tile, 4 waves in a
@@ -179,6 +182,31 @@ int fp8bg_gemm(const void* A, const void* B,
                const fp8bg_config* cfg, int32_t num_cus,
                float* ws, int64_t ws_elems,
                void* stream);
+
+/*
+ * fp8bg_gemm without a workspace argument, for callers that cannot allocate
+ * device memory (code under hipGraph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  Same kernels,
+ * plan and results as fp8bg_gemm (bitwise), with the split-K partials in a
+ * static per-GPU scratch array of FP8BG_SCRATCH_ELEMS fp32 (16 MiB; the
+ * packaged gfx950 tables need at most 1 Mi elements on any route).  Calls
+ * nothing that allocates: no hipMalloc/hipFree, no library allocator.
+ *   - A launch whose plan needs more than FP8BG_SCRATCH_ELEMS workspace
+ *     elements returns FP8BG_ERR_SCRATCH before anything is enqueued.
+ *   - Runs on the current device; a non-NULL `stream` must belong to it
+ *     (else FP8BG_ERR_DEVICE).  The scratch address is looked up once per
+ *     device.
+ *   - Every call on one GPU shares that GPU's scratch, which keeps the last
+ *     split call's partials.  Nothing in it needs clearing (each split call
+ *     writes all the partials it reads), but split calls that overlap on one
+ *     GPU (different streams, or threads without ordering) race on it.
+ */
+#define FP8BG_SCRATCH_ELEMS (1 << 22)
+int fp8bg_gemm_noalloc(const void* A, const void* B,
+                       const float* As, int64_t as_stride_m, int64_t as_stride_k,
+                       const float* Bs, int64_t bs_stride_n, int64_t bs_stride_k,
+                       const void* bias, void* C, int32_t M, int32_t N, int32_t K,
+                       const fp8bg_config* cfg, int32_t num_cus, void* stream);
 
 /*
  * Per-token-group activation quantisation (stream-ordered, no sync):
