@@ -70,6 +70,10 @@ constexpr int ring_scale_slices(int tw, int tt, int nwave) {
     return (tt + (tw + 127) / 128 + tw / 2 + 64 * nwave - 1) / (64 * nwave);
 }
 constexpr int kNumXcd = 8;            // MI355X: 8 XCDs, workgroups dealt round-robin
+// Word 3 of a gfx9 buffer resource for raw byte-offset loads (no format
+// conversion, no swizzle); word 2 holds the size in bytes, loads past it
+// return zero.
+constexpr int kBufferFlags = 0x00020000;
 
 struct KArgs {
     const uint8_t* A;      // [M, K] e4m3, row stride K
@@ -442,7 +446,8 @@ template <int R>
 struct WaveRole {
     static constexpr int value = R;
 };
-// whether a ring step issues the loads of the groups ST - KU ahead
+// whether a ring step issues the loads of the groups ST - KU ahead (also
+// used as a compile-time yes/no flag elsewhere)
 template <bool B>
 struct Loads {
     static constexpr bool value = B;
@@ -543,7 +548,15 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
     // those are loaded twice, by two waves, into the same LDS bytes with the
     // same data, so every wave issues NJ loads per group and the vmcnt
     // bookkeeping stays uniform. ----
-    const uint8_t* sbase[NJ];
+    // The operand loads go through buffer resources of A and B (byte
+    // offsets below 2^32: the host refuses M*K or N*K beyond that): the
+    // lane's fixed offset is the VGPR offset and the group's advance the
+    // SGPR offset, so a group issues no per-lane address arithmetic.
+    const __amdgpu_buffer_rsrc_t rsA =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.A, (short)0, (int)((uint32_t)a.M * (uint32_t)a.K), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rsB =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.B, (short)0, (int)((uint32_t)a.N * (uint32_t)a.K), kBufferFlags);
+    bool from_b[NJ];
     uint32_t soff[NJ];
     int dblk[NJ];
 #pragma unroll
@@ -553,13 +566,11 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         dblk[j] = b;
         const int row = 8 * b + (lane >> 3);
         const int chunk = (lane & 7) ^ swz(row, a.swz);
-        if (8 * b < TW) {
-            sbase[j] = a.B;
+        from_b[j] = 8 * b < TW;                   // wave-uniform
+        if (from_b[j])
             soff[j] = (uint32_t)min(w0 + row, a.N - 1) * (uint32_t)a.K + chunk * 16;
-        } else {
-            sbase[j] = a.A;
+        else
             soff[j] = (uint32_t)min(t0 + row - TW, a.M - 1) * (uint32_t)a.K + chunk * 16;
-        }
     }
     // scale slot q = 64 * (h * NWAVE + wave) + lane of slice h: As of token
     // t0 + q, then Bs of weight block w0 / 128 + (q - TT) for the NBS blocks
@@ -586,9 +597,9 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         }
     }
     auto dma_block = [&](int j, int g, int stage) {
-        __builtin_amdgcn_global_load_lds(
-            (const void*)(sbase[j] + (uint32_t)(soff[j] + (uint32_t)g * kGroupK)),
-            FP8BG_LDS_PTR(lds + stage * STAGE + dblk[j] * 1024), 16, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(from_b[j] ? rsB : rsA,
+                                                 FP8BG_LDS_PTR(lds + stage * STAGE + dblk[j] * 1024), 16,
+                                                 soff[j], (uint32_t)g * kGroupK, 0, 0);
     };
     auto dma_scales = [&](int g, int stage) {
 #pragma unroll
@@ -609,11 +620,16 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[w][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
+    // Operand reads: lane l reads row r0 + (l & 15) of a 16-row block at
+    // chunks c0 and c0 ^ 1.  The lane's two byte offsets inside a stage are
+    // fixed; the block's row r0 (wave-uniform) becomes the read's immediate
+    // offset, so a group adds only the stage base to the two lane offsets.
     const int c0 = ((lane >> 4) * 2) ^ swz(lane & 15, a.swz);
-    auto opread = [&](const unsigned char* st, int row) -> i32x8 {
-        const unsigned char* base = st + row * kRowBytes;
-        const i32x4 lo = *(const i32x4*)(base + (c0 << 4));
-        const i32x4 hi = *(const i32x4*)(base + ((c0 ^ 1) << 4));
+    const uint32_t lane_lo = (lane & 15) * kRowBytes + (c0 << 4);
+    const uint32_t lane_hi = (lane & 15) * kRowBytes + ((c0 ^ 1) << 4);
+    auto opread = [&](const unsigned char* st, int r0) -> i32x8 {
+        const i32x4 lo = *(const i32x4*)(st + lane_lo + r0 * kRowBytes);
+        const i32x4 hi = *(const i32x4*)(st + lane_hi + r0 * kRowBytes);
         return (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
 
@@ -651,12 +667,12 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         // fenced so the LDS serves them in that order: the first MFMA waits
         // for four reads, not for all of them (about 1% fewer cycles on the
         // largest tiles, up to 4% on the mid-size ones).
-        i32x8 top = opread(st, TW + wv_t * WTT + (lane & 15));
+        i32x8 top = opread(st, TW + wv_t * WTT);
         __builtin_amdgcn_sched_barrier(0);
         i32x8 wop[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-            wop[w] = opread(st, wv_w * WTW + w * 16 + (lane & 15));
+            wop[w] = opread(st, wv_w * WTW + w * 16);
             __builtin_amdgcn_sched_barrier(0);
         }
         const float sb = sc[TT + (w0 % 128 + wv_w * WTW) / 128];
@@ -676,7 +692,7 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
             i32x8 top_next = top;
             float sa_next = sa_t;
             if (t > 0 && t + 1 < NT) {
-                top_next = opread(st, TW + wv_t * WTT + (t + 1) * 16 + (lane & 15));
+                top_next = opread(st, TW + wv_t * WTT + (t + 1) * 16);
                 sa_next = sc[wv_t * WTT + (t + 1) * 16 + (lane & 15)];
             }
 #pragma unroll
@@ -699,7 +715,7 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
                 if (t > 0) promote(acc[w][t - 1], prev[w], s_prev);
                 if (t == 0 && w == 0 && NT > 1) {
                     __builtin_amdgcn_sched_barrier(0);
-                    top_next = opread(st, TW + wv_t * WTT + 16 + (lane & 15));
+                    top_next = opread(st, TW + wv_t * WTT + 16);
                     sa_next = sc[wv_t * WTT + 16 + (lane & 15)];
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -723,41 +739,63 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
     // LDS operations run in order) and stores them while the MFMAs of the
     // later blocks run, instead of after a barrier at the end:
     // 1-5% faster on tiles from 128x128 up (smaller ones, whose epilogue is
-    // short, do not gain), bitwise the same output.  The 256x256 tile takes
-    // this path only in fp8bg_ring_dp: beside the split tiles' epilogue its
-    // registers spill at the end of the loop.  The products
-    // are promoted right after their own MFMAs here (no second set of product
-    // registers).
-    constexpr bool kEarlyC = ring_has_dp(TW, TT, KF, KU, WK) && (DPO || !kPrio);
+    // short, do not gain), bitwise the same output.  Only fp8bg_ring_dp (the
+    // kernel of launches without split tiles) takes this path: beside the
+    // split tiles' end epilogue the large tiles' registers spill.  The
+    // products are promoted right after their own MFMAs here (no second set
+    // of product registers).
+    constexpr bool kEarlyC = ring_has_dp(TW, TT, KF, KU, WK) && DPO;
     static_assert(!kEarlyC || NWAVE * 16 * ROWB <= STAGE, "C staging inside the idle stage");
-    auto group_last = [&](int i) __attribute__((always_inline)) {
+    // Packing of a finished token block: with a bias, C is rounded, the bias
+    // added and the sum rounded again (every value canonicalised); without
+    // one, a single wave-wide unordered compare per block decides whether
+    // any value needs NaN canonicalisation at all, and otherwise the
+    // conversion instruction alone packs it.
+    auto group_last = [&](int i, auto has_bias) __attribute__((always_inline)) {
+        constexpr bool HB = decltype(has_bias)::value;
         const unsigned char* st = lds + (i % ST) * STAGE;
         const float* sc = (const float*)(st + OPS);
         unsigned char* reg = lds + ((i + ST - 1) % ST) * STAGE + wave * (16 * ROWB);
         const uint16_t* bl = (const uint16_t*)(st + OPS + (TT + NBS) * 4);
-        i32x8 top = opread(st, TW + wv_t * WTT + (lane & 15));
+        i32x8 top = opread(st, TW + wv_t * WTT);
         i32x8 wop[NW];
 #pragma unroll
-        for (int w = 0; w < NW; ++w) wop[w] = opread(st, wv_w * WTW + w * 16 + (lane & 15));
+        for (int w = 0; w < NW; ++w) wop[w] = opread(st, wv_w * WTW + w * 16);
         const float sb = sc[TT + (w0 % 128 + wv_w * WTW) / 128];
         const int r = lane & 15, qd = lane >> 4;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const float s_t = sc[wv_t * WTT + t * 16 + (lane & 15)] * sb;
             i32x8 top_next = top;
-            if (t + 1 < NT) top_next = opread(st, TW + wv_t * WTT + (t + 1) * 16 + (lane & 15));
+            if (t + 1 < NT) top_next = opread(st, TW + wv_t * WTT + (t + 1) * 16);
 #pragma unroll
             for (int w = 0; w < NW; ++w) promote(acc[w][t], mfma16x16x128(wop[w], top), s_t);
             top = top_next;
             // rows of token block t: chunk c of row r at slot c ^ (r % CPR)
             int mb = t0 + wv_t * WTT + t * 16;
             asm volatile("" : "+v"(mb));          // computed here, not hoisted
+            uint2 pk[NW];
+            if constexpr (HB) {
+#pragma unroll
+                for (int w = 0; w < NW; ++w)
+                    pk[w] = out_bf16x4v(acc[w][t], true, *(const uint2*)(bl + wv_w * WTW + w * 16 + qd * 4));
+            } else {
+                bool nan = false;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) {
+                    pk[w] = pack_bf16x4_nonan(acc[w][t]);
+                    nan = nan | __builtin_isunordered(acc[w][t][0], acc[w][t][1]) |
+                          __builtin_isunordered(acc[w][t][2], acc[w][t][3]);
+                }
+                if (__builtin_amdgcn_ballot_w64(nan) != 0) {
+                    asm volatile("" ::: "memory");    // stays a branch: not computed speculatively
+#pragma unroll
+                    for (int w = 0; w < NW; ++w) pk[w] = pack_bf16x4(acc[w][t]);
+                }
+            }
 #pragma unroll
             for (int w = 0; w < NW; ++w)
-                *(uint2*)(reg + r * ROWB + (((2 * w + (qd >> 1)) ^ (r % CPR)) << 4) + (qd & 1) * 8) =
-                    a.bias ? out_bf16x4v(acc[w][t], true,
-                                         *(const uint2*)(bl + wv_w * WTW + w * 16 + qd * 4))
-                           : pack_bf16x4(acc[w][t]);
+                *(uint2*)(reg + r * ROWB + (((2 * w + (qd >> 1)) ^ (r % CPR)) << 4) + (qd & 1) * 8) = pk[w];
 #pragma unroll
             for (int h = 0; h < (16 * CPR + 63) / 64; ++h) {
                 const int idx = lane + 64 * h;
@@ -820,7 +858,10 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
             if (kPrio) __builtin_amdgcn_s_setprio(0);
-            group_last(kcount - 1);
+            if (a.bias)
+                group_last(kcount - 1, Loads<true>{});
+            else
+                group_last(kcount - 1, Loads<false>{});
             return;
         }
         if (kPrio && wv_t) {
@@ -1041,34 +1082,43 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
 #pragma unroll
         for (int t = 0; t < NTB; ++t) acc[w][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    // This wave's groups: k_lo + wave + S*j, j = 0 .. J-1.
+    // This wave's groups: k_lo + wave + S*j, j = 0 .. J-1, in batches of U.
+    // Where the doubled operand registers fit (kPipe), the next batch's loads
+    // are issued before the current batch is computed, so a wave has two
+    // batches of weight bytes in flight instead of one round trip per batch
+    // (the accumulation order, and so the result, is the same either way).
     const int J = wave < kcount ? (kcount - 1 - wave) / S + 1 : 0;
-    for (int j0 = 0; j0 < J; j0 += U) {
+    struct Batch {
         i32x8 wv[U][NWB], tv[U][NTB];
         i32x4 xr[QA ? U : 1][QA ? NTB : 1][4];
         float sa[U][NTB], sb[U][NWB];
+    };
+    // Loads are issued unconditionally (a group index past the wave's last
+    // group is clamped to it; compute skips those), so they form straight-
+    // line code and each batch's computation waits only for its own loads.
+    auto load = [&](Batch& b, int j0) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (j0 + u < J) {
-                const int g = k_lo + wave + S * (j0 + u);
+            const int g = k_lo + wave + S * min(j0 + u, J - 1);
 #pragma unroll
-                for (int w = 0; w < NWB; ++w) {
-                    wv[u][w] = load_op(wp[w] + (size_t)g * kGroupK);
-                    sb[u][w] = bsp[w][(int64_t)g * a.bs_sk];
-                }
+            for (int w = 0; w < NWB; ++w) {
+                b.wv[u][w] = load_op(wp[w] + (size_t)g * kGroupK);
+                b.sb[u][w] = bsp[w][(int64_t)g * a.bs_sk];
+            }
 #pragma unroll
-                for (int t = 0; t < NTB; ++t) {
-                    if (QA) {
+            for (int t = 0; t < NTB; ++t) {
+                if (QA) {
 #pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            xr[u][t][c] = *(const i32x4*)(xp[t] + (size_t)g * kGroupK + 8 * c);
-                    } else {
-                        tv[u][t] = load_op(tp[t] + (size_t)g * kGroupK);
-                        sa[u][t] = asp[t][(int64_t)g * a.as_sk];
-                    }
+                    for (int c = 0; c < 4; ++c)
+                        b.xr[u][t][c] = *(const i32x4*)(xp[t] + (size_t)g * kGroupK + 8 * c);
+                } else {
+                    b.tv[u][t] = load_op(tp[t] + (size_t)g * kGroupK);
+                    b.sa[u][t] = asp[t][(int64_t)g * a.as_sk];
                 }
             }
         }
+    };
+    auto compute = [&](Batch& b, int j0) __attribute__((always_inline)) {
         if (QA) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -1081,8 +1131,8 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                         for (int c = 0; c < 4; ++c)
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
-                                v[8 * c + 2 * i] = __uint_as_float((uint32_t)xr[u][t][c][i] << 16);
-                                v[8 * c + 2 * i + 1] = __uint_as_float((uint32_t)xr[u][t][c][i] & 0xffff0000u);
+                                v[8 * c + 2 * i] = __uint_as_float((uint32_t)b.xr[u][t][c][i] << 16);
+                                v[8 * c + 2 * i + 1] = __uint_as_float((uint32_t)b.xr[u][t][c][i] & 0xffff0000u);
                             }
                         float amax = 0.f;
                         bool nan = false;
@@ -1106,8 +1156,8 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                             d = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * i + 2] * rcp, v[4 * i + 3] * rcp, d, true);
                             o[i] = d;
                         }
-                        tv[u][t] = o;
-                        sa[u][t] = sc;
+                        b.tv[u][t] = o;
+                        b.sa[u][t] = sc;
                         const int m = t0 + 16 * t + r;
                         if (qa_write && m < a.M) {
                             uint8_t* qd = a.q_out + (size_t)m * a.K + (size_t)g * kGroupK + 32 * q;
@@ -1126,7 +1176,39 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                 for (int w = 0; w < NWB; ++w)
 #pragma unroll
                     for (int t = 0; t < NTB; ++t)
-                        promote(acc[w][t], mfma16x16x128(wv[u][w], tv[u][t]), sa[u][t] * sb[u][w]);
+                        promote(acc[w][t], mfma16x16x128(b.wv[u][w], b.tv[u][t]), b.sa[u][t] * b.sb[u][w]);
+            }
+        }
+    };
+    // operand VGPRs of one batch: weights, tokens (and their bf16 source);
+    // two batches and the accumulators must leave room for the rest
+    constexpr int kBatchRegs = U * (NWB + NTB + (QA ? 2 * NTB : 0)) * 8;
+    constexpr bool kPipe = 2 * kBatchRegs + 4 * NWB * NTB <= 160;
+    if (J > 0) {
+        if constexpr (kPipe) {
+            // batches alternate between b0 and b1; the wave's last batch is
+            // computed on an early exit, so no load sits under a branch
+            Batch b0, b1;
+            load(b0, 0);
+            for (int j0 = 0;; j0 += 2 * U) {
+                if (j0 + U >= J) {
+                    compute(b0, j0);
+                    break;
+                }
+                load(b1, j0 + U);
+                compute(b0, j0);
+                if (j0 + 2 * U >= J) {
+                    compute(b1, j0 + U);
+                    break;
+                }
+                load(b0, j0 + 2 * U);
+                compute(b1, j0 + U);
+            }
+        } else {
+            for (int j0 = 0; j0 < J; j0 += U) {
+                Batch b;
+                load(b, j0);
+                compute(b, j0);
             }
         }
     }
@@ -1286,7 +1368,8 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(4, 2, 4, 2) X(4, 2, 8, 1) X(4, 2, 8, 2)                                  \
     X(1, 4, 4, 2) X(1, 4, 8, 1) X(1, 4, 8, 2)                                  \
     X(2, 4, 4, 2) X(2, 4, 8, 1) X(2, 4, 8, 2)                                  \
-    X(4, 4, 4, 1) X(4, 4, 8, 1) X(4, 4, 4, 2)
+    X(4, 4, 4, 1) X(4, 4, 8, 1) X(4, 4, 4, 2)                                  \
+    X(1, 1, 4, 4) X(2, 1, 4, 4) X(4, 1, 4, 4)
 
 // ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 //        K slices)
@@ -1318,11 +1401,13 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(64, 64, 2, 2, 8, 0, 4, 1)
 
 // skinny with the fused activation quantiser: the 16-token (NT = 1) tiles
-// (4, 1, 8, 4) left out: with the bf16 staging it needs more than 256 VGPRs
+// (4, 1, 8, 4) and (4, 1, 4, 4) left out: with the bf16 staging they need more
+// than 256 VGPRs
 #define FP8BG_SKINNY_QA(X)                                                     \
     X(1, 1, 4, 1) X(1, 1, 4, 2) X(1, 1, 8, 1) X(1, 1, 8, 2) X(1, 1, 8, 4)      \
     X(2, 1, 4, 1) X(2, 1, 4, 2) X(2, 1, 8, 1) X(2, 1, 8, 2) X(2, 1, 8, 4)      \
-    X(4, 1, 4, 1) X(4, 1, 4, 2) X(4, 1, 8, 1) X(4, 1, 8, 2)
+    X(4, 1, 4, 1) X(4, 1, 4, 2) X(4, 1, 8, 1) X(4, 1, 8, 2)                    \
+    X(1, 1, 4, 4) X(2, 1, 4, 4)
 
 struct Instance {
     int kind, tw, tt, ww, wt, wk, unroll, stages, kf, threads;

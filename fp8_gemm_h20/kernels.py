@@ -53,12 +53,15 @@ SKINNY = (
     (1, 4, 4, 2), (1, 4, 8, 1), (1, 4, 8, 2),
     (2, 4, 4, 2), (2, 4, 8, 1), (2, 4, 8, 2),
     (4, 4, 4, 1), (4, 4, 8, 1), (4, 4, 4, 2),
+    # four waves with four 128-K groups in flight each: every group of a
+    # K=2048 wave in one batch (decode)
+    (1, 1, 4, 4), (2, 1, 4, 4), (4, 1, 4, 4),
 )
 # skinny instances as (block_w, block_t, waves_k, unroll)
 SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
-# skinny with the activation quantiser fused (16-token tiles, except the one
+# skinny with the activation quantiser fused (16-token tiles, except the two
 # that would spill); must match FP8BG_SKINNY_QA in csrc/fp8bg.hip
-SKINNY_QA = tuple(c for c in SKINNY if c[1] == 1 and c != (4, 1, 8, 4))
+SKINNY_QA = tuple(c for c in SKINNY if c[1] == 1 and c not in ((4, 1, 8, 4), (4, 1, 4, 4)))
 # ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 #        K slices)
 RING = (
