@@ -11,7 +11,7 @@ from pathlib import Path
 
 LIB_NAME = "libfp8bg.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 OK = 0
 ERR_SHAPE = 1
@@ -33,6 +33,10 @@ KIND_RING = 2
 SPLIT_NONE = 0
 SPLIT_TAIL = 1
 SPLIT_FULL = 2
+SPLIT_LAST = 3
+
+# uint32 tile counters at the start of every split-K workspace (FP8BG_COUNTERS)
+COUNTERS = 4096
 
 FLAG_SCALE_LDS = 0x1
 FLAG_XCD_REMAP = 0x2

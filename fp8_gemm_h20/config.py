@@ -27,7 +27,7 @@ from .engine import KERNELS, NATIVE
 _CONFIG_DIR = Path(__file__).with_name("configs")
 _PROFILES = ("35b_tp1", "122b_tp4")
 _POLICIES = ("log_nearest", "nearby_equal_tiles")
-_SPLIT_MODES = ("none", "tail", "full")
+_SPLIT_MODES = ("none", "tail", "full")     # ring and tiled ("last": skinny only)
 
 
 def available_profiles():
@@ -68,7 +68,7 @@ def _native_ok(impl, c, k):
                 (k // 128 // (split if (k // 128) % split == 0 else 1)) % ku == 0)
     if impl == "skinny":
         mode = c.get("SPLIT_MODE", "none")
-        return (mode in ("none", "full") and
+        return (mode in ("none", "full", "last") and
                 (tw, tt, c.get("WAVES_K", 8), c.get("UNROLL", 1)) in SKINNY_TILES)
     kf = 2 if impl == "shortk" else 0
     if c.get("SPLIT_MODE", "full") not in _SPLIT_MODES:

@@ -57,6 +57,7 @@ namespace {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kGroupK = 128;          // K elements per scale group
@@ -74,6 +75,9 @@ constexpr int kNumXcd = 8;            // MI355X: 8 XCDs, workgroups dealt round-
 // conversion, no swizzle); word 2 holds the size in bytes, loads past it
 // return zero.
 constexpr int kBufferFlags = 0x00020000;
+// Cache-policy operand of buffer loads and stores: SC1, device scope (the
+// access is coherent across the XCDs' private L2 caches).
+constexpr int kDeviceScope = 16;
 
 struct KArgs {
     const uint8_t* A;      // [M, K] e4m3, row stride K
@@ -83,6 +87,9 @@ struct KArgs {
     uint16_t* C;           // [M, N] bf16, row stride N
     const uint16_t* bias;  // [N] bf16 or nullptr
     float* ws;             // split-K partials [split tile][split][tt][tw]
+                           // (FP8BG_SPLIT_LAST: [split tile][split][block][lane] f32x4)
+    uint32_t* cnt;         // FP8BG_SPLIT_LAST tile counters (zero between calls)
+    int split_last;        // partials reduced in the GEMM kernel by the last workgroup
     int64_t as_sm, as_sk, bs_sn, bs_sk;
     int M, N, K;
     int tw, tt;            // workgroup tile (weight rows, tokens)
@@ -1182,8 +1189,9 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     };
     // operand VGPRs of one batch: weights, tokens (and their bf16 source);
     // two batches and the accumulators must leave room for the rest
+    // (16 waves per workgroup leave 128 VGPRs per wave, fewer waves 256)
     constexpr int kBatchRegs = U * (NWB + NTB + (QA ? 2 * NTB : 0)) * 8;
-    constexpr bool kPipe = 2 * kBatchRegs + 4 * NWB * NTB <= 160;
+    constexpr bool kPipe = 2 * kBatchRegs + 4 * NWB * NTB <= (S >= 16 ? 72 : 160);
     if (J > 0) {
         if constexpr (kPipe) {
             // batches alternate between b0 and b1; the wave's last batch is
@@ -1213,6 +1221,14 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
         }
     }
 
+    // FP8BG_SPLIT_LAST partials: block b of split sidx of tile, one f32x4 per
+    // lane (byte offsets below 2^31: the host checks the plan)
+    const __amdgpu_buffer_rsrc_t ws_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.ws, (short)0, 0x7fffffff, kBufferFlags);
+    auto last_off = [&](int tl_, int sp, int b) -> uint32_t {
+        return (uint32_t)((((tl_ * a.split + sp) * NB + b) * 64 + lane) * 16);
+    };
+
     // Fixed-order sum of the S wave partials through LDS.
 #pragma unroll
     for (int w = 0; w < NWB; ++w)
@@ -1231,13 +1247,52 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
         }
         const int w = b / NTB, t = b % NTB;
         const int tl = 16 * t + r, wl = 16 * w + 4 * q;
-        if (a.split > 1) {
+        if (a.split > 1 && a.split_last) {
+            // device-scope store (coherent across the XCDs' L2s): the tile's
+            // last workgroup may run on another XCD
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, s), ws_rsrc,
+                                                   last_off(tile, sidx, b), 0, kDeviceScope);
+        } else if (a.split > 1) {
             float* mine = a.ws + ((size_t)tile * a.split + sidx) * (size_t)(TW * TT);
             *(f32x4*)(mine + tl * TW + wl) = s;
         } else {
             const int m = t0 + tl, n = w0 + wl;
             if (m < a.M && n < a.N) *(uint2*)(a.C + (size_t)m * a.N + n) = out_bf16x4(s, a.bias, n);
         }
+    }
+    if (a.split > 1 && a.split_last) {
+        // The tile's partials are summed by the workgroup that completes its
+        // count: every workgroup's partial stores have completed (vmcnt 0, at
+        // device scope) before its count, so the last one's device-scope
+        // loads, issued after its count returned, see them all.  The sum runs
+        // in split order, as fp8bg_split_reduce's; the counter is left at
+        // zero for the next call (and for hipGraph replays).
+        __shared__ int is_last;
+        asm volatile("" ::: "memory");
+        wait_vmcnt<0>();
+        asm volatile("" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0)
+            is_last = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      (uint32_t)(a.split - 1);
+        __syncthreads();
+        if (!is_last) return;
+        for (int b = wave; b < NB; b += S) {
+            f32x4 s = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(ws_rsrc, last_off(tile, 0, b), 0, kDeviceScope));
+            for (int k = 1; k < a.split; ++k) {
+                const f32x4 v = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(ws_rsrc, last_off(tile, k, b), 0, kDeviceScope));
+                s[0] += v[0];
+                s[1] += v[1];
+                s[2] += v[2];
+                s[3] += v[3];
+            }
+            const int w = b / NTB, t = b % NTB;
+            const int m = t0 + 16 * t + r, n = w0 + 16 * w + 4 * q;
+            if (m < a.M && n < a.N) *(uint2*)(a.C + (size_t)m * a.N + n) = out_bf16x4(s, a.bias, n);
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -1369,7 +1424,9 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(1, 4, 4, 2) X(1, 4, 8, 1) X(1, 4, 8, 2)                                  \
     X(2, 4, 4, 2) X(2, 4, 8, 1) X(2, 4, 8, 2)                                  \
     X(4, 4, 4, 1) X(4, 4, 8, 1) X(4, 4, 4, 2)                                  \
-    X(1, 1, 4, 4) X(2, 1, 4, 4) X(4, 1, 4, 4)
+    X(1, 1, 4, 4) X(2, 1, 4, 4) X(4, 1, 4, 4)                                  \
+    X(1, 1, 16, 1) X(1, 1, 16, 2) X(2, 1, 16, 1) X(2, 1, 16, 2) X(4, 1, 16, 1) \
+    X(1, 2, 16, 1) X(2, 2, 16, 1) X(1, 4, 16, 1)
 
 // ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 //        K slices)
@@ -1401,13 +1458,14 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(64, 64, 2, 2, 8, 0, 4, 1)
 
 // skinny with the fused activation quantiser: the 16-token (NT = 1) tiles
-// (4, 1, 8, 4) and (4, 1, 4, 4) left out: with the bf16 staging they need more
-// than 256 VGPRs
+// ((4, 1, 8, 4), (4, 1, 4, 4) and (4, 1, 16, 1) left out: with the bf16
+// staging they need more VGPRs than their wave count leaves)
 #define FP8BG_SKINNY_QA(X)                                                     \
     X(1, 1, 4, 1) X(1, 1, 4, 2) X(1, 1, 8, 1) X(1, 1, 8, 2) X(1, 1, 8, 4)      \
     X(2, 1, 4, 1) X(2, 1, 4, 2) X(2, 1, 8, 1) X(2, 1, 8, 2) X(2, 1, 8, 4)      \
     X(4, 1, 4, 1) X(4, 1, 4, 2) X(4, 1, 8, 1) X(4, 1, 8, 2)                    \
-    X(1, 1, 4, 4) X(2, 1, 4, 4)
+    X(1, 1, 4, 4) X(2, 1, 4, 4)                                                \
+    X(1, 1, 16, 1) X(1, 1, 16, 2) X(2, 1, 16, 1) X(2, 1, 16, 2)
 
 struct Instance {
     int kind, tw, tt, ww, wt, wk, unroll, stages, kf, threads;
@@ -1606,7 +1664,7 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     const int ki = find_instance(cfg);
     if (ki < 0) return FP8BG_ERR_CONFIG;
     if (cfg->split < 1 || cfg->group_t < 1 || num_cus < 1) return FP8BG_ERR_CONFIG;
-    if (cfg->split_mode < FP8BG_SPLIT_NONE || cfg->split_mode > FP8BG_SPLIT_FULL) return FP8BG_ERR_CONFIG;
+    if (cfg->split_mode < FP8BG_SPLIT_NONE || cfg->split_mode > FP8BG_SPLIT_LAST) return FP8BG_ERR_CONFIG;
     if (cfg->flags & ~(FP8BG_FLAG_SCALE_LDS | FP8BG_FLAG_XCD_REMAP | FP8BG_FLAG_SWZ8 |
                        FP8BG_FLAG_SWZPAIR))
         return FP8BG_ERR_CONFIG;
@@ -1622,13 +1680,20 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
 
     int split = (cfg->split_mode == FP8BG_SPLIT_NONE || k.kf) ? 1 : cfg->split;
     if (kg % split) split = 1;  // reference baseline_gluon.py:274-276
-    if (skinny && split > 1 && cfg->split_mode != FP8BG_SPLIT_FULL) return FP8BG_ERR_CONFIG;
+    const bool last = cfg->split_mode == FP8BG_SPLIT_LAST;
+    if (last && !skinny) return FP8BG_ERR_CONFIG;
+    if (skinny && split > 1 && cfg->split_mode == FP8BG_SPLIT_TAIL) return FP8BG_ERR_CONFIG;
     const int64_t tiles_w = (N + k.tw - 1) / k.tw;
     const int64_t tiles_t = ((int64_t)M + k.tt - 1) / k.tt;
     const int64_t tiles = tiles_w * tiles_t;
     int64_t n_split = 0;
     if (split > 1) n_split = cfg->split_mode == FP8BG_SPLIT_TAIL ? tiles % num_cus : tiles;
     if (n_split == 0) split = 1;
+    // the in-kernel reduction: one counter per split tile, partial byte
+    // offsets below 2^31
+    if (last && split > 1 &&
+        (n_split > FP8BG_COUNTERS || n_split * split * (int64_t)k.tw * k.tt * 4 > 0x7fffffffLL))
+        return FP8BG_ERR_SHAPE;
     // a ring kernel computing KU groups per barrier needs whole multiples of
     // KU in every workgroup's K range (kg / split divides kg)
     if (ring && (kg / split) % k.unroll) return FP8BG_ERR_CONFIG;
@@ -1655,8 +1720,8 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     plan->n_dp = (int32_t)n_dp;
     plan->n_split = (int32_t)n_split;
     plan->grid = (int32_t)grid;
-    plan->launches = n_split ? 2 : 1;
-    plan->ws_elems = n_split * split * (int64_t)k.tw * k.tt;
+    plan->launches = n_split && !last ? 2 : 1;
+    plan->ws_elems = n_split ? FP8BG_COUNTERS + n_split * split * (int64_t)k.tw * k.tt : 0;
     plan->lds_bytes = (int32_t)lds;
     plan->threads = k.threads;
     plan->kernel_id = ki;
@@ -1696,7 +1761,10 @@ int gemm_enqueue(const void* A, const void* B, const float* As, int64_t as_strid
     a.Bs = Bs;
     a.C = (uint16_t*)C;
     a.bias = (const uint16_t*)bias;
-    a.ws = ws;
+    // workspace: the tile counters, then the partials
+    a.cnt = (uint32_t*)ws;
+    a.ws = ws ? ws + FP8BG_COUNTERS : nullptr;
+    a.split_last = cfg->split_mode == FP8BG_SPLIT_LAST;
     a.as_sm = as_stride_m;
     a.as_sk = as_stride_k;
     a.bs_sn = bs_stride_n;
@@ -1718,7 +1786,7 @@ int gemm_enqueue(const void* A, const void* B, const float* As, int64_t as_strid
     hipStream_t s = (hipStream_t)stream;
     k.launch(dim3(p.grid), shm, s, a);
     if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
-    if (p.n_split > 0) {
+    if (p.n_split > 0 && !a.split_last) {
         const int parts = reduce_parts(p, k, num_cus);
         hipLaunchKernelGGL(fp8bg_split_reduce, dim3(p.n_split * parts), dim3(kThreads), 0, s, a,
                            k.kind == FP8BG_KIND_SKINNY ? 1 : 0, parts);
@@ -1821,7 +1889,9 @@ int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps, const void* B
     a.Bs = Bs;
     a.C = (uint16_t*)C;
     a.bias = (const uint16_t*)bias;
-    a.ws = ws;
+    a.cnt = (uint32_t*)ws;
+    a.ws = ws ? ws + FP8BG_COUNTERS : nullptr;
+    a.split_last = cfg->split_mode == FP8BG_SPLIT_LAST;
     a.bs_sn = bs_stride_n;
     a.bs_sk = bs_stride_k;
     a.M = M;
@@ -1845,7 +1915,7 @@ int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps, const void* B
     hipStream_t s = (hipStream_t)stream;
     k.launch(dim3(p.grid), 0, s, a);
     if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
-    if (p.n_split > 0) {
+    if (p.n_split > 0 && !a.split_last) {
         const int parts = reduce_parts(p, k, num_cus);
         hipLaunchKernelGGL(fp8bg_split_reduce, dim3(p.n_split * parts), dim3(kThreads), 0, s, a, 1,
                            parts);

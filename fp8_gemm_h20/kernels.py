@@ -14,7 +14,8 @@ Two families of config dicts are accepted:
 * gfx950-native entries written by this package's tuner:
   - impl "tiled": BLOCK_W, BLOCK_T, WAVES_W, WAVES_T, SPLIT, SPLIT_MODE,
     GROUP_SIZE_M, SCALE_LDS, XCD_REMAP, LDS_SWIZZLE (LDS-tiled kernel);
-  - impl "skinny": BLOCK_W, BLOCK_T, WAVES_K, UNROLL, SPLIT, SPLIT_MODE,
+  - impl "skinny": BLOCK_W, BLOCK_T, WAVES_K, UNROLL, SPLIT, SPLIT_MODE
+    ("none", "full" or "last": the split reduced inside the kernel),
     XCD_REMAP (small-M kernel, waves split K);
   - impl "ring": BLOCK_W, BLOCK_T, WAVES_W, WAVES_T, STAGES, K_UNROLL, WAVES_K, SPLIT,
     SPLIT_MODE, GROUP_SIZE_M, XCD_REMAP, LDS_SWIZZLE (direct-to-LDS ring
@@ -56,12 +57,17 @@ SKINNY = (
     # four waves with four 128-K groups in flight each: every group of a
     # K=2048 wave in one batch (decode)
     (1, 1, 4, 4), (2, 1, 4, 4), (4, 1, 4, 4),
+    # sixteen waves splitting K: one or two groups per wave, for shapes with
+    # few weight tiles (narrow N) whose waves would otherwise make several
+    # dependent memory round trips
+    (1, 1, 16, 1), (1, 1, 16, 2), (2, 1, 16, 1), (2, 1, 16, 2), (4, 1, 16, 1),
+    (1, 2, 16, 1), (2, 2, 16, 1), (1, 4, 16, 1),
 )
 # skinny instances as (block_w, block_t, waves_k, unroll)
 SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
-# skinny with the activation quantiser fused (16-token tiles, except the two
+# skinny with the activation quantiser fused (16-token tiles, except the three
 # that would spill); must match FP8BG_SKINNY_QA in csrc/fp8bg.hip
-SKINNY_QA = tuple(c for c in SKINNY if c[1] == 1 and c not in ((4, 1, 8, 4), (4, 1, 4, 4)))
+SKINNY_QA = tuple(c for c in SKINNY if c[1] == 1 and c not in ((4, 1, 8, 4), (4, 1, 4, 4), (4, 1, 16, 1)))
 # ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 #        K slices)
 RING = (
@@ -96,7 +102,8 @@ RING = (
     # 64x64 with 2x2 waves (two weight blocks per wave)
     (64, 64, 2, 2, 8, 0, 4, 1),
 )
-SPLIT_MODES = {"none": _lib.SPLIT_NONE, "tail": _lib.SPLIT_TAIL, "full": _lib.SPLIT_FULL}
+SPLIT_MODES = {"none": _lib.SPLIT_NONE, "tail": _lib.SPLIT_TAIL, "full": _lib.SPLIT_FULL,
+               "last": _lib.SPLIT_LAST}
 
 
 def default_waves(block_w, block_t, k_fixed=0):
@@ -189,8 +196,9 @@ _NUM_CUS = {}
 
 
 class SplitBuffers:
-    """Split-K workspace (fp32) of one (device, stream) pair (reference
-    baseline_gluon.py:229-244).
+    """Split-K workspace of one (device, stream) pair (reference
+    baseline_gluon.py:229-244): COUNTERS uint32 tile counters, zero when
+    allocated and left zero by every call, then the fp32 partials.
 
     Launches on one stream are ordered, so every split-K GEMM on that stream
     can share one workspace; kernels on different streams never share.
@@ -216,7 +224,7 @@ class SplitBuffers:
             size = max(ws_elems, self.MIN_WS, 2 * (self.ws.numel() if self.ws is not None else 0))
             if self.ws is not None:
                 self.retired.append(self.ws)
-            self.ws = torch.empty(size, device=self.device, dtype=torch.float32)
+            self.ws = torch.zeros(size, device=self.device, dtype=torch.float32)
         return self.ws
 
 

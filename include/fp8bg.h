@@ -43,7 +43,7 @@ extern "C" {
 
 /* ABI version returned by fp8bg_version(); bumped on any signature or struct
  * change. */
-#define FP8BG_ABI_VERSION 6
+#define FP8BG_ABI_VERSION 7
 
 /* ---- kernel kinds --------------------------------------------------------- */
 /* LDS-tiled kernel: a block_w x block_t workgroup tile, 4 waves in a
@@ -51,7 +51,7 @@ extern "C" {
  * Replaces the reference's tiled kernels (kernels/baseline_triton.py:28-81,
  * kernels/baseline_gluon.py:94-211, kernels/kernel_v2.py:94-291). */
 #define FP8BG_KIND_TILED  0
-/* Small-M kernel: no LDS staging; waves_k waves (4 or 8) split the K groups
+/* Small-M kernel: no LDS staging; waves_k waves (4, 8 or 16) split the K groups
  * of one block_w x block_t tile, `unroll` groups in flight per wave, partials
  * summed in fixed wave order.  The reference's SWAP_AB small-M role
  * (kernels/baseline_gluon.py:77-83). */
@@ -77,6 +77,19 @@ extern "C" {
 /* In both split modes the fp32 partials go to the caller's workspace and a
  * second kernel on the same stream sums them in fixed split order and writes
  * bf16 (deterministic, replay-safe, no atomics or counters). */
+/* Full split reduced inside the GEMM kernel (skinny kernel only): each
+ * workgroup writes its partial tile with device-scope stores and counts it in
+ * the tile's counter; the workgroup that completes the count sums the
+ * partials in split order (bitwise the FP8BG_SPLIT_FULL result), writes C and
+ * resets the counter.  One launch instead of two (the reference's
+ * self-resetting counters, kernels/baseline_gluon.py:194-209, with the
+ * summation order fixed).  At most FP8BG_COUNTERS split tiles. */
+#define FP8BG_SPLIT_LAST 3
+
+/* Split-K workspace layout (every split mode): FP8BG_COUNTERS uint32 tile
+ * counters, then the fp32 partials.  The counters must be zero before a
+ * workspace's first use; every call leaves them zero. */
+#define FP8BG_COUNTERS 4096
 
 /* ---- config flags --------------------------------------------------------- */
 /* Stage the tile's activation scales As[tile rows, k range] in LDS once per
@@ -101,7 +114,7 @@ typedef struct fp8bg_config {
     int32_t block_t;    /* tokens (M) per workgroup tile */
     int32_t waves_w;    /* tiled/ring: waves along N inside the tile */
     int32_t waves_t;    /* tiled/ring: waves along M inside the tile */
-    int32_t waves_k;    /* skinny: waves splitting K inside a workgroup (4 or 8);
+    int32_t waves_k;    /* skinny: waves splitting K inside a workgroup (4, 8 or 16);
                            ring: K slices of waves_w x waves_t waves (1, 2 or 4;
                            0 means 1) */
     int32_t unroll;     /* skinny: 128-K groups in flight per wave;
@@ -111,7 +124,8 @@ typedef struct fp8bg_config {
     int32_t split;      /* cross-workgroup K split factor, in 128-K groups;
                            normalised to 1 when it does not divide K/128
                            (baseline_gluon.py:274-276) */
-    int32_t split_mode; /* FP8BG_SPLIT_* (skinny: NONE or FULL) */
+    int32_t split_mode; /* FP8BG_SPLIT_* (skinny: NONE, FULL or LAST; tiled
+                           and ring: NONE, TAIL or FULL) */
     int32_t group_t;    /* tiled: token-tile swizzle group (GROUP_SIZE_M
                            semantics, baseline_triton.py:36-45); >= 1 */
     int32_t flags;      /* FP8BG_FLAG_* */
@@ -135,7 +149,8 @@ typedef struct fp8bg_plan {
     int32_t n_split;    /* tiles split over `split` workgroups */
     int32_t grid;       /* workgroups of the GEMM kernel = n_dp + n_split * split */
     int32_t launches;   /* kernels enqueued: 1, or 2 with the split-K reduction */
-    int64_t ws_elems;   /* fp32 workspace elements needed (0 if no split) */
+    int64_t ws_elems;   /* workspace elements needed (0 if no split):
+                           FP8BG_COUNTERS + the fp32 partials */
     int32_t lds_bytes;  /* LDS used per workgroup */
     int32_t threads;    /* threads per workgroup */
     int32_t kernel_id;  /* index of the compiled kernel instance */
@@ -164,11 +179,12 @@ int fp8bg_config_supported(const fp8bg_config* cfg);
  *   block_fp8_gemm_v2          (kernels/kernel_v2.py:339-376)
  *   block_fp8_gemm_scale_tma   (kernels/kernel_scale_tma.py:356-396)
  *   shortk                     (kernels/kernel_shortk.py:46-54)
- * with the caller owning C (bf16 [M,N], row stride N) and the fp32 split-K
- * workspace `ws` (>= plan.ws_elems elements, 16-byte aligned; unused and may
- * be NULL when plan.n_split == 0).  Calls that share `ws` must be ordered
- * (same stream); a captured hipGraph keeps using the `ws` it was captured
- * with, so that buffer must outlive the graph.
+ * with the caller owning C (bf16 [M,N], row stride N) and the split-K
+ * workspace `ws` (>= plan.ws_elems 4-byte elements, 16-byte aligned, laid out
+ * as FP8BG_COUNTERS zero counters then fp32 partials; unused and may be NULL
+ * when plan.n_split == 0).  Calls that share `ws` must be ordered (same
+ * stream); a captured hipGraph keeps using the `ws` it was captured with, so
+ * that buffer must outlive the graph.
  * Scale strides are in elements.  A, B and C must be 16-byte aligned.
  * `bias` (bf16 [N], 8-byte aligned, or NULL) is added in the epilogue exactly
  * as the reference adapter's separate `out + bias` does it
@@ -197,9 +213,11 @@ int fp8bg_gemm(const void* A, const void* B,
  *     (else FP8BG_ERR_DEVICE).  The scratch address is looked up once per
  *     device.
  *   - Every call on one GPU shares that GPU's scratch, which keeps the last
- *     split call's partials.  Nothing in it needs clearing (each split call
- *     writes all the partials it reads), but split calls that overlap on one
- *     GPU (different streams, or threads without ordering) race on it.
+ *     split call's partials.  Nothing in it needs clearing: each split call
+ *     writes all the partials it reads, and the tile counters of
+ *     FP8BG_SPLIT_LAST start at zero (the array is zero when the library
+ *     loads) and are left zero by every call.  Split calls that overlap on
+ *     one GPU (different streams, or threads without ordering) race on it.
  */
 #define FP8BG_SCRATCH_ELEMS (1 << 22)
 int fp8bg_gemm_noalloc(const void* A, const void* B,
