@@ -1,6 +1,6 @@
 """Calibration of the GPU this runs on: the FP8 MFMA rate and the streaming
-read rate it sustains, measured with the library's two calibration kernels
-(fp8bg_calib_mfma, fp8bg_calib_read).  They are reported next to the
+read and write rates it sustains, measured with the library's calibration
+kernels (fp8bg_calib_mfma, fp8bg_calib_read, fp8bg_calib_write).  They are reported next to the
 published peaks (5.0 PFLOP/s dense FP8, 8 TB/s HBM) that the roofline
 fractions divide by, as the share of those peaks the chip itself reaches.
 """
@@ -70,3 +70,24 @@ def read_rate(torch, device, stream, nbytes=1 << 30, workgroups_per_cu=2, reps=5
     torch.cuda.synchronize(device)
     return {"GBps": round(nbytes / us / 1e3, 1), "us": round(us, 1), "bytes": nbytes,
             "workgroups": wgs}
+
+
+def write_rate(torch, device, stream, nbytes=1 << 30, workgroups_per_cu=2, reps=5, nontemporal=True):
+    """Streaming write rate into an nbytes buffer, in GB/s: 16-byte stores,
+    non-temporal by default as the GEMM kernels write C.  Checks that every
+    word holds the written value."""
+    lib = _lib.lib()
+    wgs = _num_cus(device) * workgroups_per_cu
+    buf = torch.zeros(nbytes // 4, dtype=torch.int32, device=device)
+    value = 0x3F803F80                               # two bf16 1.0
+
+    def launch():
+        _lib.check(lib.fp8bg_calib_write(buf.data_ptr(), buf.numel() * 4, value, wgs,
+                                         1 if nontemporal else 0, stream.cuda_stream))
+    with torch.cuda.stream(stream):
+        us = _time(torch, stream, launch, reps)
+    torch.cuda.synchronize(device)
+    if not bool((buf == value).all()):
+        raise RuntimeError("fp8bg_calib_write: wrong contents")
+    return {"GBps": round(nbytes / us / 1e3, 1), "us": round(us, 1), "bytes": nbytes,
+            "workgroups": wgs, "nontemporal": bool(nontemporal)}

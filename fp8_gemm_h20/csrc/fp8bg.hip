@@ -78,6 +78,8 @@ constexpr int kBufferFlags = 0x00020000;
 // Cache-policy operand of buffer loads and stores: SC1, device scope (the
 // access is coherent across the XCDs' private L2 caches).
 constexpr int kDeviceScope = 16;
+// The same operand's NT bit: a non-temporal (streaming) access.
+constexpr int kNonTemporal = 2;
 
 struct KArgs {
     const uint8_t* A;      // [M, K] e4m3, row stride K
@@ -89,7 +91,10 @@ struct KArgs {
     float* ws;             // split-K partials [split tile][split][tt][tw]
                            // (FP8BG_SPLIT_LAST: [split tile][split][block][lane] f32x4)
     uint32_t* cnt;         // FP8BG_SPLIT_LAST tile counters (zero between calls)
-    int split_last;        // partials reduced in the GEMM kernel by the last workgroup
+    int split_last;        // split tiles reduced in the GEMM kernel (selects its instance)
+    int kcount;            // 128-K groups per workgroup: K / 128 / split
+    uint2 div_split;       // fast_div reciprocals of split and tiles_t
+    uint2 div_tiles_t;
     int64_t as_sm, as_sk, bs_sn, bs_sk;
     int M, N, K;
     int tw, tt;            // workgroup tile (weight rows, tokens)
@@ -188,6 +193,20 @@ __device__ __forceinline__ i32x8 load_op(const uint8_t* p) {
     const i32x4 lo = *(const i32x4*)p;
     const i32x4 hi = *(const i32x4*)(p + 16);
     return (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// n / d for 0 <= n < 2^31 as (mulhi(n, m) + n) >> l with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1 (the round-up reciprocal method), from
+// the pair {m, l} made on the host by fast_div_of(d).
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, uint2 ml) {
+    return (__umulhi(n, ml.x) + n) >> ml.y;
+}
+
+inline uint2 fast_div_of(uint32_t d) {
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    const uint64_t m = (((1ull << 32) * ((1ull << l) - d)) / d) + 1;
+    return make_uint2((uint32_t)m, l);
 }
 
 // Bijective remap of workgroup ids 0..n-1 so that ids dealt to the same XCD
@@ -590,7 +609,12 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
     for (int h = 0; h < NSC; ++h) {
         const int q = 64 * (h * NWAVE + wave) + lane;
         if (q < TT) {
-            sc_base[h] = a.As + (int64_t)min(t0 + q, a.M - 1) * a.as_sm;
+            // slot r * NT + t of a wave's WTT-token range holds token
+            // t * 16 + r: a lane's NT scales (token r of each 16-token
+            // block) are contiguous, one or two 16-byte reads per group
+            const int ql = q % WTT;
+            const int tok = q - ql + (ql % NT) * 16 + ql / NT;
+            sc_base[h] = a.As + (int64_t)min(t0 + tok, a.M - 1) * a.as_sm;
             sc_step[h] = a.as_sk;
         } else if (q < TT + NBS) {
             sc_base[h] = a.Bs + (int64_t)min(w0 / 128 + (q - TT), a.N / 128 - 1) * a.bs_sn;
@@ -683,6 +707,10 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
             __builtin_amdgcn_sched_barrier(0);
         }
         const float sb = sc[TT + (w0 % 128 + wv_w * WTW) / 128];
+        float sa[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) sa[t] = sc[wv_t * WTT + (lane & 15) * NT + t];
+        __builtin_amdgcn_sched_barrier(0);
         // Software pipeline over token blocks: block t's products go into
         // their own registers, and each MFMA is followed by the four
         // promotion FMAs of the previous block's product for the same weight
@@ -691,17 +719,12 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         // block 0, right after its first MFMA).  The scheduling fences keep
         // this order (the default schedule promotes each product right after
         // its own MFMA and stalls on it).
-        float sa_t = sc[wv_t * WTT + (lane & 15)];
         f32x4 prev[NW];
         float s_prev = 0.f;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             i32x8 top_next = top;
-            float sa_next = sa_t;
-            if (t > 0 && t + 1 < NT) {
-                top_next = opread(st, TW + wv_t * WTT + (t + 1) * 16);
-                sa_next = sc[wv_t * WTT + (t + 1) * 16 + (lane & 15)];
-            }
+            if (t > 0 && t + 1 < NT) top_next = opread(st, TW + wv_t * WTT + (t + 1) * 16);
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
                 if (LD && (j * NT) / (2 * NJ) == t) dma_block(j, g_next, s_next);
@@ -723,15 +746,13 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
                 if (t == 0 && w == 0 && NT > 1) {
                     __builtin_amdgcn_sched_barrier(0);
                     top_next = opread(st, TW + wv_t * WTT + 16);
-                    sa_next = sc[wv_t * WTT + 16 + (lane & 15)];
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
             for (int w = 0; w < NW; ++w) prev[w] = cur[w];
-            s_prev = sa_t * sb;
+            s_prev = sa[t] * sb;
             top = top_next;
-            sa_t = sa_next;
         }
 #pragma unroll
         for (int w = 0; w < NW; ++w) promote(acc[w][NT - 1], prev[w], s_prev);
@@ -770,17 +791,28 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         for (int w = 0; w < NW; ++w) wop[w] = opread(st, wv_w * WTW + w * 16);
         const float sb = sc[TT + (w0 % 128 + wv_w * WTW) / 128];
         const int r = lane & 15, qd = lane >> 4;
+        // byte offsets of the lane's C chunks inside a 16-row block
+        constexpr int HC = (16 * CPR + 63) / 64;
+        uint32_t voff[HC];
+#pragma unroll
+        for (int h = 0; h < HC; ++h) {
+            const int idx = lane + 64 * h;
+            const int row = idx / CPR, n = w0 + wv_w * WTW + (idx % CPR) * 8;
+            voff[h] = row < 16 && n < a.N ? (uint32_t)(row * a.N + n) * 2u : 0x80000000u;
+        }
+        float sa[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) sa[t] = sc[wv_t * WTT + r * NT + t];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const float s_t = sc[wv_t * WTT + t * 16 + (lane & 15)] * sb;
+            const float s_t = sa[t] * sb;
             i32x8 top_next = top;
             if (t + 1 < NT) top_next = opread(st, TW + wv_t * WTT + (t + 1) * 16);
 #pragma unroll
             for (int w = 0; w < NW; ++w) promote(acc[w][t], mfma16x16x128(wop[w], top), s_t);
             top = top_next;
             // rows of token block t: chunk c of row r at slot c ^ (r % CPR)
-            int mb = t0 + wv_t * WTT + t * 16;
-            asm volatile("" : "+v"(mb));          // computed here, not hoisted
+            const int mb = t0 + wv_t * WTT + t * 16;        // wave-uniform
             uint2 pk[NW];
             if constexpr (HB) {
 #pragma unroll
@@ -803,15 +835,26 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
 #pragma unroll
             for (int w = 0; w < NW; ++w)
                 *(uint2*)(reg + r * ROWB + (((2 * w + (qd >> 1)) ^ (r % CPR)) << 4) + (qd & 1) * 8) = pk[w];
+            // The block's 16 rows through a buffer resource based at row mb
+            // and sized to the rows that exist (below 2^31 bytes: the host
+            // checks 32 N): rows past M, and columns past N (offset 2^31),
+            // fall outside it and are dropped.
+            // (both wave-uniform; readfirstlane says so to the compiler,
+            // which otherwise builds the resource per lane in a loop)
+            const int rows = __builtin_amdgcn_readfirstlane(min(max(a.M - mb, 0), 16));
+            const uint64_t cbase = (uint64_t)(a.C + (size_t)mb * a.N);
+            const uint64_t cb = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(cbase >> 32)) << 32) |
+                                (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)cbase);
+            const __amdgpu_buffer_rsrc_t crs =
+                __builtin_amdgcn_make_buffer_rsrc((void*)cb, (short)0, rows * a.N * 2, kBufferFlags);
 #pragma unroll
-            for (int h = 0; h < (16 * CPR + 63) / 64; ++h) {
+            for (int h = 0; h < HC; ++h) {
                 const int idx = lane + 64 * h;
                 const int row = idx / CPR, c = idx % CPR;
                 if (row >= 16) continue;
                 const i32x4 v = *(const i32x4*)(reg + row * ROWB + ((c ^ (row % CPR)) << 4));
-                const int m = mb + row, n = w0 + wv_w * WTW + c * 8;
-                if (m < a.M && n < a.N)
-                    __builtin_nontemporal_store(v, (i32x4*)(a.C + (size_t)m * a.N + n));
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), crs, voff[h], 0,
+                                                       kNonTemporal);
             }
         }
     };
@@ -1031,9 +1074,15 @@ void fp8bg_ring_dp(KArgs a) {
 // reciprocal replaces the standalone quantiser's division: one multiply per
 // value instead of a division sequence, which is what makes the fused path
 // cheaper than a separate kernel.
-template <int NWB, int NTB, int S, int U, int QA>
+// MODE bits: the fused quantiser, and the in-kernel split-K reduction
+// (FP8BG_SPLIT_LAST).  The reduction is compiled only into its own instances:
+// its epilogue, even when not taken, costs the common instances registers
+// (skinny<2,1,8,1> 80 -> 86 VGPRs, one workgroup per CU fewer).
+constexpr int kSkinnyQuant = 1, kSkinnyLast = 2;
+template <int NWB, int NTB, int S, int U, int MODE>
 __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     constexpr int TW = 16 * NWB, TT = 16 * NTB, NB = NWB * NTB;
+    constexpr bool QA = MODE & kSkinnyQuant, LAST = MODE & kSkinnyLast;
     __shared__ f32x4 red[S][NB][64];
 
     const int lane = threadIdx.x & 63;
@@ -1044,19 +1093,20 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     // adjacent (and, with xcd_remap, on one XCD's L2).
     // With a cross-workgroup split (full mode only) workgroup pid computes
     // K range pid % split of tile pid / split.
+    // (divisions by the split and by tiles_t through host-computed
+    // reciprocals: the decode's first loads wait on this arithmetic)
+    // The fields are read up front and the tile decoded without branches,
+    // so the argument loads issue together instead of one round per branch.
     const int pid = blockIdx.x;
-    int tile = pid, sidx = 0;
-    if (a.split > 1) {
-        tile = pid / a.split;
-        sidx = pid % a.split;
-    } else if (a.xcd_remap) {
-        tile = xcd_remap(pid, a.tiles_w * a.tiles_t);
-    }
-    const int pt = tile % a.tiles_t, pw = tile / a.tiles_t;
+    const int split = a.split, tiles_t = a.tiles_t, remap = a.xcd_remap;
+    const int tiles = a.tiles_w * tiles_t;
+    const int kcount = a.kcount;
+    const uint2 div_split = a.div_split, div_tiles_t = a.div_tiles_t;
+    const int q_split = (int)fast_div(pid, div_split);
+    const int tile = split > 1 ? q_split : remap ? xcd_remap(pid, tiles) : pid;
+    const int sidx = split > 1 ? pid - q_split * split : 0;
+    const int pw = (int)fast_div(tile, div_tiles_t), pt = tile - pw * tiles_t;
     const int w0 = pw * TW, t0 = pt * TT;
-
-    const int KG = a.K / kGroupK;
-    const int kcount = KG / a.split;
     const int k_lo = sidx * kcount;
 
     const uint8_t* wp[NWB];
@@ -1223,9 +1273,9 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
 
     // FP8BG_SPLIT_LAST partials: block b of split sidx of tile, one f32x4 per
     // lane (byte offsets below 2^31: the host checks the plan)
-    const __amdgpu_buffer_rsrc_t ws_rsrc =
+    [[maybe_unused]] const __amdgpu_buffer_rsrc_t ws_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.ws, (short)0, 0x7fffffff, kBufferFlags);
-    auto last_off = [&](int tl_, int sp, int b) -> uint32_t {
+    [[maybe_unused]] auto last_off = [&](int tl_, int sp, int b) -> uint32_t {
         return (uint32_t)((((tl_ * a.split + sp) * NB + b) * 64 + lane) * 16);
     };
 
@@ -1247,7 +1297,7 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
         }
         const int w = b / NTB, t = b % NTB;
         const int tl = 16 * t + r, wl = 16 * w + 4 * q;
-        if (a.split > 1 && a.split_last) {
+        if constexpr (LAST) {
             // device-scope store (coherent across the XCDs' L2s): the tile's
             // last workgroup may run on another XCD
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, s), ws_rsrc,
@@ -1260,23 +1310,24 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
             if (m < a.M && n < a.N) *(uint2*)(a.C + (size_t)m * a.N + n) = out_bf16x4(s, a.bias, n);
         }
     }
-    if (a.split > 1 && a.split_last) {
+    if constexpr (LAST) {
         // The tile's partials are summed by the workgroup that completes its
         // count: every workgroup's partial stores have completed (vmcnt 0, at
         // device scope) before its count, so the last one's device-scope
         // loads, issued after its count returned, see them all.  The sum runs
         // in split order, as fp8bg_split_reduce's; the counter is left at
-        // zero for the next call (and for hipGraph replays).
-        __shared__ int is_last;
+        // zero for the next call (and for hipGraph replays).  The flag lives
+        // in red[], whose reads all precede the barrier below.
+        int* is_last = (int*)&red[0][0][0];
         asm volatile("" ::: "memory");
         wait_vmcnt<0>();
         asm volatile("" ::: "memory");
         __syncthreads();
         if (threadIdx.x == 0)
-            is_last = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            *is_last = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                       (uint32_t)(a.split - 1);
         __syncthreads();
-        if (!is_last) return;
+        if (!*is_last) return;
         for (int b = wave; b < NB; b += S) {
             f32x4 s = __builtin_bit_cast(
                 f32x4, __builtin_amdgcn_raw_buffer_load_b128(ws_rsrc, last_off(tile, 0, b), 0, kDeviceScope));
@@ -1483,7 +1534,11 @@ FP8BG_TILED(FP8BG_TILED_LAUNCHER)
 #define FP8BG_SKINNY_LAUNCHER(NW, NT, S, U)                                                  \
     static void skinny_##NW##_##NT##_##S##_##U(dim3 g, size_t shm, hipStream_t s,           \
                                                const KArgs& a) {                            \
-        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, 0>), g, dim3(64 * S), shm, s, a);     \
+        if (a.split_last)                                                                     \
+            hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kSkinnyLast>), g, dim3(64 * S), shm, \
+                               s, a);                                                         \
+        else                                                                                  \
+            hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, 0>), g, dim3(64 * S), shm, s, a); \
     }
 FP8BG_SKINNY(FP8BG_SKINNY_LAUNCHER)
 #undef FP8BG_SKINNY_LAUNCHER
@@ -1491,7 +1546,12 @@ FP8BG_SKINNY(FP8BG_SKINNY_LAUNCHER)
 #define FP8BG_SKINNY_QA_LAUNCHER(NW, NT, S, U)                                               \
     static void skinny_qa_##NW##_##NT##_##S##_##U(dim3 g, size_t shm, hipStream_t s,        \
                                                   const KArgs& a) {                         \
-        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, 1>), g, dim3(64 * S), shm, s, a);     \
+        if (a.split_last)                                                                     \
+            hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kSkinnyQuant | kSkinnyLast>), g,   \
+                               dim3(64 * S), shm, s, a);                                      \
+        else                                                                                  \
+            hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kSkinnyQuant>), g, dim3(64 * S),   \
+                               shm, s, a);                                                    \
     }
 FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_LAUNCHER)
 #undef FP8BG_SKINNY_QA_LAUNCHER
@@ -1571,7 +1631,8 @@ int find_instance(const fp8bg_config* c) {
 
 // ===========================================================================
 // Calibration kernels (measurement only): the MFMA issue rate and the
-// streaming-read rate this chip sustains, next to the published peaks.
+// streaming-read and streaming-write rates this chip sustains, next to the
+// published peaks.
 // ===========================================================================
 constexpr int kCalibMfmaPerIter = 16;
 
@@ -1622,6 +1683,29 @@ __global__ __launch_bounds__(256) void fp8bg_calib_read_kernel(const i32x4* src,
     }
     for (; i < n16; i += stride) x ^= src[i];
     out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = (uint32_t)(x[0] ^ x[1] ^ x[2] ^ x[3]);
+}
+
+// Grid-stride write of n16 16-byte words of `value`, four stores in flight
+// per lane; NT selects the non-temporal stores that the GEMM kernels use for
+// C, whose lines are not read again.
+template <bool NT>
+__global__ __launch_bounds__(256) void fp8bg_calib_write_kernel(i32x4* dst, int64_t n16, uint32_t value) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const i32x4 v = {(int)value, (int)value, (int)value, (int)value};
+    auto put = [&](int64_t j) __attribute__((always_inline)) {
+        if constexpr (NT)
+            __builtin_nontemporal_store(v, dst + j);
+        else
+            dst[j] = v;
+    };
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        put(i);
+        put(i + stride);
+        put(i + 2 * stride);
+        put(i + 3 * stride);
+    }
+    for (; i < n16; i += stride) put(i);
 }
 
 extern "C" {
@@ -1675,8 +1759,11 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     const bool skinny = k.kind == FP8BG_KIND_SKINNY;
     const bool ring = k.kind == FP8BG_KIND_RING;
     if ((skinny || ring) && (cfg->flags & FP8BG_FLAG_SCALE_LDS)) return FP8BG_ERR_CONFIG;
-    // the ring kernel addresses A and B with 32-bit byte offsets
-    if (ring && ((int64_t)M * K > 0xffffffffLL || (int64_t)N * K > 0xffffffffLL)) return FP8BG_ERR_SHAPE;
+    // the ring kernel addresses A and B with 32-bit byte offsets, and 16 rows
+    // of C with 31-bit ones
+    if (ring && ((int64_t)M * K > 0xffffffffLL || (int64_t)N * K > 0xffffffffLL ||
+                 (int64_t)N * 32 > 0x7fffffffLL))
+        return FP8BG_ERR_SHAPE;
 
     int split = (cfg->split_mode == FP8BG_SPLIT_NONE || k.kf) ? 1 : cfg->split;
     if (kg % split) split = 1;  // reference baseline_gluon.py:274-276
@@ -1764,7 +1851,7 @@ int gemm_enqueue(const void* A, const void* B, const float* As, int64_t as_strid
     // workspace: the tile counters, then the partials
     a.cnt = (uint32_t*)ws;
     a.ws = ws ? ws + FP8BG_COUNTERS : nullptr;
-    a.split_last = cfg->split_mode == FP8BG_SPLIT_LAST;
+    a.split_last = cfg->split_mode == FP8BG_SPLIT_LAST && p.n_split > 0;
     a.as_sm = as_stride_m;
     a.as_sk = as_stride_k;
     a.bs_sn = bs_stride_n;
@@ -1778,6 +1865,9 @@ int gemm_enqueue(const void* A, const void* B, const float* As, int64_t as_strid
     a.tiles_t = p.tiles_t;
     a.n_dp = p.n_dp;
     a.split = p.split;
+    a.kcount = (K / kGroupK) / p.split;
+    a.div_split = fast_div_of((uint32_t)p.split);
+    a.div_tiles_t = fast_div_of((uint32_t)p.tiles_t);
     a.group_t = cfg->group_t;
     a.xcd_remap = (cfg->flags & FP8BG_FLAG_XCD_REMAP) ? 1 : 0;
     a.scale_lds = (cfg->flags & FP8BG_FLAG_SCALE_LDS) ? 1 : 0;
@@ -1891,7 +1981,7 @@ int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps, const void* B
     a.bias = (const uint16_t*)bias;
     a.cnt = (uint32_t*)ws;
     a.ws = ws ? ws + FP8BG_COUNTERS : nullptr;
-    a.split_last = cfg->split_mode == FP8BG_SPLIT_LAST;
+    a.split_last = cfg->split_mode == FP8BG_SPLIT_LAST && p.n_split > 0;
     a.bs_sn = bs_stride_n;
     a.bs_sk = bs_stride_k;
     a.M = M;
@@ -1903,6 +1993,9 @@ int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps, const void* B
     a.tiles_t = p.tiles_t;
     a.n_dp = p.n_dp;
     a.split = p.split;
+    a.kcount = (K / kGroupK) / p.split;
+    a.div_split = fast_div_of((uint32_t)p.split);
+    a.div_tiles_t = fast_div_of((uint32_t)p.tiles_t);
     a.group_t = cfg->group_t;
     a.xcd_remap = (cfg->flags & FP8BG_FLAG_XCD_REMAP) ? 1 : 0;
     a.X = (const uint16_t*)X;
@@ -1967,6 +2060,20 @@ int fp8bg_calib_read(const void* src, int64_t bytes, uint32_t* out, int32_t work
     if ((((uintptr_t)src) & 15) || (((uintptr_t)out) & 3)) return FP8BG_ERR_ALIGN;
     hipLaunchKernelGGL(fp8bg_calib_read_kernel, dim3((unsigned)workgroups), dim3(256), 0,
                        (hipStream_t)stream, (const i32x4*)src, bytes / 16, out);
+    return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
+}
+
+int fp8bg_calib_write(void* dst, int64_t bytes, uint32_t value, int32_t workgroups, int32_t nontemporal,
+                      void* stream) {
+    if (!dst) return FP8BG_ERR_NULL;
+    if (bytes < 16 || bytes % 16 || workgroups < 1) return FP8BG_ERR_SHAPE;
+    if (((uintptr_t)dst) & 15) return FP8BG_ERR_ALIGN;
+    if (nontemporal)
+        hipLaunchKernelGGL(fp8bg_calib_write_kernel<true>, dim3((unsigned)workgroups), dim3(256), 0,
+                           (hipStream_t)stream, (i32x4*)dst, bytes / 16, value);
+    else
+        hipLaunchKernelGGL(fp8bg_calib_write_kernel<false>, dim3((unsigned)workgroups), dim3(256), 0,
+                           (hipStream_t)stream, (i32x4*)dst, bytes / 16, value);
     return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
 }
 

@@ -43,7 +43,7 @@ extern "C" {
 
 /* ABI version returned by fp8bg_version(); bumped on any signature or struct
  * change. */
-#define FP8BG_ABI_VERSION 7
+#define FP8BG_ABI_VERSION 8
 
 /* ---- kernel kinds --------------------------------------------------------- */
 /* LDS-tiled kernel: a block_w x block_t workgroup tile, 4 waves in a
@@ -105,7 +105,7 @@ extern "C" {
 #define FP8BG_FLAG_SWZPAIR   0x8   /* swz = (r >> 1) & 7 */
 
 /*
- * Kernel configuration: one gfx950 table entry (fp8_gemm_h20/configs/*.json).
+ * Kernel configuration: one gfx950 table entry (fp8_gemm_h20/configs/<profile>.json).
  * Replaces the reference's per-entry `config` dict (fp8_gemm_h20/config.py:80-91).
  */
 typedef struct fp8bg_config {
@@ -281,7 +281,8 @@ int fp8bg_e4m3_encode_host(const float* x, uint8_t* out, int64_t n);
 /*
  * Calibration kernels: what this chip sustains, measured next to the
  * published peaks (no reference counterpart; the measurement plan for this
- * path asks for an MFMA-only and a streaming-read calibration).
+ * path asks for an MFMA-only, a streaming-read and a streaming-write
+ * calibration).
  *
  * fp8bg_calib_mfma: `workgroups` workgroups of 256 threads (4 waves); each
  * wave issues 16 FP8 16x16x128 MFMAs per iteration (65536 flops each), for
@@ -293,12 +294,19 @@ int fp8bg_e4m3_encode_host(const float* x, uint8_t* out, int64_t n);
  * fp8bg_calib_read: reads `bytes` (a multiple of 16, src 16-byte aligned)
  * with `workgroups` workgroups of 256 threads and writes workgroups * 256
  * uint32 words whose XOR equals the XOR of all 32-bit words of src.
+ *
+ * fp8bg_calib_write: fills `bytes` (a multiple of 16, dst 16-byte aligned)
+ * with the 32-bit `value`, `workgroups` workgroups of 256 threads issuing
+ * 16-byte stores; nontemporal != 0 uses the non-temporal stores the GEMM
+ * kernels write C with.
  */
 #define FP8BG_CALIB_MAX_ITERS 8192
 int fp8bg_calib_mfma(const int32_t* codes, float* out, int32_t workgroups, int32_t iters,
                      void* stream);
 int fp8bg_calib_read(const void* src, int64_t bytes, uint32_t* out, int32_t workgroups,
                      void* stream);
+int fp8bg_calib_write(void* dst, int64_t bytes, uint32_t value, int32_t workgroups, int32_t nontemporal,
+                      void* stream);
 
 /* Static message for an error code. */
 const char* fp8bg_strerror(int code);
