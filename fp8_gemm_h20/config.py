@@ -15,6 +15,12 @@ Differences, all additive:
   route unchanged.
 * `select_in(data, M, N, K)` / `supports_in(...)` apply the policy to any
   validated table dict, e.g. a table loaded with `load_profile(path)`.
+* An optional `fused_entries` section ({"N,K": {"M": entry}}, M the decode
+  anchors) names, per anchor, the skinny configuration of the fused
+  quantiser + GEMM launch that `linear()` takes for bf16 activations, with
+  its measured time ("anchor_us"), the two-kernel time ("two_kernel_us") and
+  whether the fused launch is used by default ("use").  `select_fused`
+  routes M to the log-nearest anchor, or to no fused entry above the largest.
 """
 import copy
 import json
@@ -133,6 +139,30 @@ def validate_config(data):
                 raise ValueError(f"Invalid shape/table: {nk}")
             for m, entry in table.items():
                 _check_entry(field, nk, k, m, entry, policy)
+    for nk, table in data.get("fused_entries", {}).items():
+        if nk not in shapes or not table:
+            raise ValueError(f"Invalid fused shape/table: {nk}")
+        for m, entry in table.items():
+            _check_fused_entry(nk, m, entry)
+
+
+def _check_fused_entry(nk, m, entry):
+    from .kernels import SKINNY_QA
+    where = f"fused {nk}/{m}"
+    if not 1 <= int(m) <= 16384 or entry.get("impl") != "skinny" or not isinstance(entry.get("use"), bool):
+        raise ValueError(f"Invalid entry: {where}")
+    c = entry.get("config", {})
+    try:
+        inst = (c["BLOCK_W"] // 16, c["BLOCK_T"] // 16, c.get("WAVES_K", 8), c.get("UNROLL", 1))
+    except (KeyError, TypeError):
+        raise ValueError(f"Invalid tile: {where}") from None
+    if (c["BLOCK_W"] % 16 or c["BLOCK_T"] % 16 or inst not in SKINNY_QA
+            or c.get("SPLIT_MODE", "none") not in ("none", "full", "last") or c.get("SPLIT", 1) < 1):
+        raise ValueError(f"Invalid tile: {where}")
+    for key in ("anchor_us", "two_kernel_us"):
+        us = entry.get(key)
+        if not isinstance(us, (int, float)) or not math.isfinite(us) or us <= 0:
+            raise ValueError(f"Measured latency must be positive: {where}")
 
 
 def load_profile(path):
@@ -200,6 +230,30 @@ def select_in(data, m, n, k):
         method = "log_nearest"
     anchor = _log_nearest(table, m)
     return table[anchor], {"method": method, "anchor": int(anchor)}
+
+
+def select_fused_in(data, m, n, k):
+    """The fused-quantiser entry for (M, N, K): the log-nearest anchor of the
+    shape's fused_entries, None above the largest anchor or where the
+    profile has no fused table for the shape."""
+    table = data.get("fused_entries", {}).get(f"{n},{k}")
+    if not table or m > max(int(a) for a in table):
+        return None
+    return table[str(m)] if str(m) in table else table[_log_nearest(table, m)]
+
+
+def _has_fused_table(profile, n, k):
+    return f"{n},{k}" in _profile(profile).get("fused_entries", {})
+
+
+@lru_cache(maxsize=4096)
+def _select_fused(profile, m, n, k):
+    return select_fused_in(_profile(profile), m, n, k)
+
+
+def select_fused(profile, m, n, k):
+    """Return a copy of the fused entry for (M, N, K), or None."""
+    return copy.deepcopy(_select_fused(profile, m, n, k))
 
 
 @lru_cache(maxsize=4096)

@@ -188,6 +188,16 @@ __device__ __forceinline__ void promote(f32x4& acc, const f32x4& p, float s) {
     acc[3] = __builtin_fmaf(p[3], s, acc[3]);
 }
 
+// The first promotion of an accumulator: fma(p, s, +0), bitwise what promote
+// gives on a zeroed accumulator (including the sign of zero), without the
+// register moves that zero it.
+__device__ __forceinline__ void promote_first(f32x4& acc, const f32x4& p, float s) {
+    acc[0] = __builtin_fmaf(p[0], s, 0.0f);
+    acc[1] = __builtin_fmaf(p[1], s, 0.0f);
+    acc[2] = __builtin_fmaf(p[2], s, 0.0f);
+    acc[3] = __builtin_fmaf(p[3], s, 0.0f);
+}
+
 // 32 operand bytes of one lane: two 16-byte global loads.
 __device__ __forceinline__ i32x8 load_op(const uint8_t* p) {
     const i32x4 lo = *(const i32x4*)p;
@@ -478,6 +488,11 @@ template <bool B>
 struct Loads {
     static constexpr bool value = B;
 };
+// whether a ring step holds each K slice's first group
+template <bool B>
+struct First {
+    static constexpr bool value = B;
+};
 
 // Workgroup tile TW weight rows x TT tokens, WW x WT waves.  Each 128-K group
 // of the stacked [weights; tokens] tile (TW + TT rows of 128 bytes) is copied
@@ -645,11 +660,11 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         dma_scales(g, stage);
     };
 
+    // The first barrier step initialises the accumulators (promote_first):
+    // every path through the loops below starts with a First<true> step, so
+    // nothing zeroes them (a zeroing branch for one-step launches would be
+    // merged into every path by the compiler).
     f32x4 acc[NW][NT];
-#pragma unroll
-    for (int w = 0; w < NW; ++w)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[w][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
     // Operand reads: lane l reads row r0 + (l & 15) of a 16-row block at
     // chunks c0 and c0 ^ 1.  The lane's two byte offsets inside a stage are
@@ -688,9 +703,10 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
     // and the older one for the rest (about 2% faster; no effect on smaller
     // tiles, so they keep one role).
     constexpr bool kPrio = WT == 2 && TW * TT >= 256 * 256;
-    auto group = [&](int i, int g_next, int s_next, auto role, auto load) {
+    auto group = [&](int i, int g_next, int s_next, auto role, auto load, auto first) {
         constexpr int R = decltype(role)::value;
         constexpr bool LD = decltype(load)::value;
+        constexpr bool FIRST = decltype(first)::value;
         const unsigned char* st = lds + (i % ST) * STAGE;
         const float* sc = (const float*)(st + OPS);
         // The group's first operands are read in the order the first token
@@ -742,7 +758,10 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
 #pragma unroll
             for (int w = 0; w < NW; ++w) {
                 cur[w] = mfma16x16x128(wop[w], top);
-                if (t > 0) promote(acc[w][t - 1], prev[w], s_prev);
+                if (t > 0) {
+                    if (FIRST) promote_first(acc[w][t - 1], prev[w], s_prev);
+                    else promote(acc[w][t - 1], prev[w], s_prev);
+                }
                 if (t == 0 && w == 0 && NT > 1) {
                     __builtin_amdgcn_sched_barrier(0);
                     top_next = opread(st, TW + wv_t * WTT + 16);
@@ -755,7 +774,10 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
             top = top_next;
         }
 #pragma unroll
-        for (int w = 0; w < NW; ++w) promote(acc[w][NT - 1], prev[w], s_prev);
+        for (int w = 0; w < NW; ++w) {
+            if (FIRST) promote_first(acc[w][NT - 1], prev[w], s_prev);
+            else promote(acc[w][NT - 1], prev[w], s_prev);
+        }
     };
 
     // Tiles with one group per barrier write C from the last group itself
@@ -861,7 +883,7 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
 
     // One barrier step: groups i .. i + KU - 1, with (load) or without the
     // loads of groups i + ST - KU .. i + ST - 1.
-    auto step = [&](int i, auto role, auto load) {
+    auto step = [&](int i, auto role, auto load, auto first) {
         // Groups i .. i + KU - 1 are complete once at most the DMA
         // instructions of the ST - 2 KU later groups are outstanding (vmcnt
         // retires in issue order; a wave loads only its slice's groups, 1 in
@@ -881,7 +903,10 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
             // both belong to this wave's slice
             const int u = uk * WK + ks;
             const int g = i + ST - KU + u;
-            group(i + u, min(k_lo + g, g_last), g % ST, role, load);
+            if (decltype(first)::value && uk == 0)
+                group(i + u, min(k_lo + g, g_last), g % ST, role, load, First<true>{});
+            else
+                group(i + u, min(k_lo + g, g_last), g % ST, role, load, First<false>{});
         }
     };
     // The last step is peeled off outside the loop (a second copy inside the
@@ -892,8 +917,11 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         // the last step is dispatched after the loop, and the C-writing one
         // returns right away (a path that rejoined the epilogue would keep
         // the epilogue's registers alive through it)
+        // (the host launches fp8bg_ring_dp, and the ring kernels that have
+        // this path take it, only where a tile has more than one step)
         auto main_loop = [&](auto role) {
-            for (int i = 0; i + KU < kcount; i += KU) step(i, role, Loads<true>{});
+            step(0, role, Loads<true>{}, First<true>{});
+            for (int i = KU; i + KU < kcount; i += KU) step(i, role, Loads<true>{}, First<false>{});
         };
         if (kPrio && wv_t) {
             main_loop(WaveRole<1>{});
@@ -915,15 +943,20 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
             return;
         }
         if (kPrio && wv_t) {
-            step(kcount - KU, WaveRole<1>{}, Loads<false>{});
+            step(kcount - KU, WaveRole<1>{}, Loads<false>{}, First<false>{});
         } else {
-            step(kcount - KU, WaveRole<0>{}, Loads<false>{});
+            step(kcount - KU, WaveRole<0>{}, Loads<false>{}, First<false>{});
         }
     } else {
         auto main_loop = [&](auto role) {
-#pragma unroll (KF ? KF / KU - 1 : 1)
-            for (int i = 0; i + KU < kcount; i += KU) step(i, role, Loads<true>{});
-            step(kcount - KU, role, Loads<false>{});
+            if (kcount > KU) {
+                step(0, role, Loads<true>{}, First<true>{});
+#pragma unroll (KF > 2 * KU ? KF / KU - 2 : 1)
+                for (int i = KU; i + KU < kcount; i += KU) step(i, role, Loads<true>{}, First<false>{});
+                step(kcount - KU, role, Loads<false>{}, First<false>{});
+            } else {
+                step(0, role, Loads<false>{}, First<true>{});
+            }
         };
         if (kPrio && wv_t) {
             main_loop(WaveRole<1>{});
@@ -1312,9 +1345,13 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     }
     if constexpr (LAST) {
         // The tile's partials are summed by the workgroup that completes its
-        // count: every workgroup's partial stores have completed (vmcnt 0, at
-        // device scope) before its count, so the last one's device-scope
-        // loads, issued after its count returned, see them all.  The sum runs
+        // count (the reference's last-arriver reduction, kernels/
+        // baseline_gluon.py:194-209): every workgroup's partial stores have
+        // completed (vmcnt 0, at device scope) before its count, so the last
+        // one's device-scope loads, issued after its count returned, see them
+        // all.  Device-scope stores and loads instead of release / acquire
+        // fences: on this chip an agent-scope fence writes back or
+        // invalidates the XCD's whole L2.  The sum runs
         // in split order, as fp8bg_split_reduce's; the counter is left at
         // zero for the next call (and for hipGraph replays).  The flag lives
         // in red[], whose reads all precede the barrier below.
@@ -1508,15 +1545,22 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(128, 160, 2, 2, 3, 0, 1, 1) X(128, 96, 2, 2, 4, 0, 1, 1)    \
     X(64, 64, 2, 2, 8, 0, 4, 1)
 
-// skinny with the fused activation quantiser: the 16-token (NT = 1) tiles
-// ((4, 1, 8, 4), (4, 1, 4, 4) and (4, 1, 16, 1) left out: with the bf16
-// staging they need more VGPRs than their wave count leaves)
+// skinny with the fused activation quantiser: the 16-, 32- and 64-token
+// tiles ((4, 1, 8, 4), (4, 1, 4, 4), (4, 1, 16, 1), (2, 4, 8, 2), (1, 4, 16, 1)
+// and the 4 x 4 tiles left out: with the bf16 staging they need more VGPRs
+// than their wave count leaves)
 #define FP8BG_SKINNY_QA(X)                                                     \
     X(1, 1, 4, 1) X(1, 1, 4, 2) X(1, 1, 8, 1) X(1, 1, 8, 2) X(1, 1, 8, 4)      \
     X(2, 1, 4, 1) X(2, 1, 4, 2) X(2, 1, 8, 1) X(2, 1, 8, 2) X(2, 1, 8, 4)      \
     X(4, 1, 4, 1) X(4, 1, 4, 2) X(4, 1, 8, 1) X(4, 1, 8, 2)                    \
+    X(1, 2, 4, 2) X(1, 2, 8, 1) X(1, 2, 8, 2)                                  \
+    X(2, 2, 4, 2) X(2, 2, 8, 1) X(2, 2, 8, 2)                                  \
+    X(4, 2, 4, 2) X(4, 2, 8, 1) X(4, 2, 8, 2)                                  \
+    X(1, 4, 4, 2) X(1, 4, 8, 1) X(1, 4, 8, 2)                                  \
+    X(2, 4, 4, 2) X(2, 4, 8, 1)                                                \
     X(1, 1, 4, 4) X(2, 1, 4, 4)                                                \
-    X(1, 1, 16, 1) X(1, 1, 16, 2) X(2, 1, 16, 1) X(2, 1, 16, 2)
+    X(1, 1, 16, 1) X(1, 1, 16, 2) X(2, 1, 16, 1) X(2, 1, 16, 2)                \
+    X(1, 2, 16, 1) X(2, 2, 16, 1)
 
 struct Instance {
     int kind, tw, tt, ww, wt, wk, unroll, stages, kf, threads;
@@ -1560,7 +1604,7 @@ FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_LAUNCHER)
     static void ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF##_##KU##_##WK(                   \
         dim3 g, size_t shm, hipStream_t s, const KArgs& a) {                                  \
         if constexpr (ring_has_dp(TW, TT, KF, KU, WK)) {                                      \
-            if (a.n_dp == (int)g.x) {                                                         \
+            if (a.n_dp == (int)g.x && a.kcount > KU) {                                        \
                 hipLaunchKernelGGL((fp8bg_ring_dp<TW, TT, WW, WT, ST, KF, KU, WK>), g,       \
                                    dim3(64 * WW * WT * WK), shm, s, a);                       \
                 return;                                                                       \

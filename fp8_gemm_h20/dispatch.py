@@ -1,5 +1,5 @@
 """Validated public entry point (reference fp8_gemm_h20/dispatch.py:5-30)."""
-from .config import _select
+from .config import _has_fused_table, _select, _select_fused
 from .engine import run
 
 
@@ -85,13 +85,15 @@ def linear(x, B, Bs, *, profile="35b_tp1", bias=None, eps=1e-10, fused=None):
     does not cover raise ValueError (the adapter's own fallback decision
     stays with the caller, as `supports` answers it).
 
-    Where the profile's entry for (M, N, K) is a 16-token skinny
-    configuration (decode sizes), the quantiser runs inside the GEMM kernel
-    (one launch instead of two, fp8bg_gemm_bf16a); its codes are
-    e4m3(x * (1/s)) rather than e4m3(x / s), equal except on rare rounding
-    ties of the two quotients.  fused=False forces the two-kernel path,
-    fused=True requires the fused one (ValueError if the entry does not
-    allow it).
+    At decode sizes the quantiser can run inside the GEMM kernel (one launch
+    instead of two, fp8bg_gemm_bf16a); its codes are e4m3(x * (1/s)) rather
+    than e4m3(x / s), equal except on rare rounding ties of the two
+    quotients.  Where the profile has a fused table for (N, K), its entry for
+    M decides: the fused launch runs when it measured faster than the two
+    kernels ("use").  Without one, the fused launch runs where the matmul
+    entry itself is a skinny configuration with a fused instance.
+    fused=False forces the two-kernel path, fused=True the fused one
+    (ValueError where no fused configuration applies).
     """
     import torch
     from . import kernels
@@ -99,24 +101,37 @@ def linear(x, B, Bs, *, profile="35b_tp1", bias=None, eps=1e-10, fused=None):
     if fused is not False and x.dtype == torch.bfloat16 and x.is_cuda and x.shape[-1] == k \
             and x.numel() > 0:
         m = x.numel() // k
-        entry, _ = _select(profile, m, n, k)
-        ok = kernels.fused_config_ok(entry) and eps >= 1e-30
+        cfg, use = _fused_choice(profile, m, n, k)
+        ok = cfg is not None and eps >= 1e-30
         if fused and not ok:
-            raise ValueError("the profile entry for this shape is not a 16-token skinny "
-                             "configuration; the fused linear does not apply")
-        if ok:
+            raise ValueError("no fused-quantiser configuration for this shape in the profile; "
+                             "the fused linear does not apply")
+        if ok and (use or fused):
             _check_weights(B, Bs, x.device, bias)
             x2 = x.reshape(-1, k)
             if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
                 x2 = x2.clone(memory_format=torch.contiguous_format)
             with torch.cuda.device(x.device):
-                out = kernels.linear_fused(x2, B, Bs, dict(entry["config"]), eps, bias=bias)
+                out = kernels.linear_fused(x2, B, Bs, cfg, eps, bias=bias)
             return out.view(*x.shape[:-1], n)
     elif fused:
         raise ValueError("fused linear needs bf16 CUDA activations with last dim K")
     q, s = quantize_act(x, eps=eps)
     out = matmul(q, B, s, Bs, profile=profile, bias=bias)
     return out.view(*x.shape[:-1], n)
+
+
+def _fused_choice(profile, m, n, k):
+    """(config, use) of the fused-quantiser launch for (M, N, K): from the
+    profile's fused table where it has one for (N, K), else the matmul entry
+    when that is a skinny configuration with a fused instance; (None, False)
+    where neither applies."""
+    from . import kernels
+    if _has_fused_table(profile, n, k):
+        entry = _select_fused(profile, m, n, k)
+        return (None, False) if entry is None else (dict(entry["config"]), entry["use"])
+    entry, _ = _select(profile, m, n, k)
+    return (dict(entry["config"]), True) if kernels.fused_config_ok(entry) else (None, False)
 
 
 def _check_weights(B, Bs, device, bias):

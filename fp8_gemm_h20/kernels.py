@@ -65,9 +65,12 @@ SKINNY = (
 )
 # skinny instances as (block_w, block_t, waves_k, unroll)
 SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
-# skinny with the activation quantiser fused (16-token tiles, except the three
-# that would spill); must match FP8BG_SKINNY_QA in csrc/fp8bg.hip
-SKINNY_QA = tuple(c for c in SKINNY if c[1] == 1 and c not in ((4, 1, 8, 4), (4, 1, 4, 4), (4, 1, 16, 1)))
+# skinny with the activation quantiser fused (16-, 32- and 64-token tiles,
+# except those whose bf16 staging would spill); must match FP8BG_SKINNY_QA in
+# csrc/fp8bg.hip
+SKINNY_QA = tuple(c for c in SKINNY
+                  if c not in ((4, 1, 8, 4), (4, 1, 4, 4), (4, 1, 16, 1), (2, 4, 8, 2), (1, 4, 16, 1))
+                  and c[0] * c[1] <= 8)
 # ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 #        K slices)
 RING = (
@@ -254,12 +257,26 @@ def _workspace(dev, ws_elems):
     return bufs.get(ws_elems)
 
 
+def check_operands(M, N, K, B, As, Bs, bias=None, out=None):
+    """The kernels take M, N, K and raw pointers; operands whose shapes
+    disagree with them would be read or written out of bounds, so they are
+    refused here (ValueError) before anything is launched."""
+    if (tuple(B.shape) != (N, K) or (As is not None and tuple(As.shape) != (M, K // 128))
+            or tuple(Bs.shape) != (N // 128, K // 128)
+            or (bias is not None and tuple(bias.shape) != (N,))
+            or (out is not None and tuple(out.shape) != (M, N))):
+        raise ValueError(f"operand shapes disagree with M,N,K={M},{N},{K}: "
+                         f"B{tuple(B.shape)} As{None if As is None else tuple(As.shape)} "
+                         f"Bs{tuple(Bs.shape)}")
+
+
 def launch(A, B, As, Bs, cstruct, bias=None, out=None):
     """Enqueue the kernel(s) described by `cstruct` into `out` (allocated
     when None); `bias` is an optional bf16 [N] added in the epilogue."""
     import torch
     M, K = A.shape
     N = B.shape[0]
+    check_operands(M, N, K, B, As, Bs, bias, out)
     dev = A.device
     cus = num_cus(dev)
     plan = _lib.make_plan(M, N, K, cstruct, cus)
@@ -297,12 +314,14 @@ def quant_act(x2, m, k, eps, column_major_scales):
 def linear_fused(x2, B, Bs, config, eps, bias=None, out=None, keep_quantized=False):
     """Decode-size linear in one launch: the skinny kernel with the activation
     quantiser fused (C ABI fp8bg_gemm_bf16a).  `x2` is a [M, K] bf16 view with
-    unit column stride; `config` a skinny table entry with BLOCK_T == 16.
+    unit column stride; `config` a skinny configuration of a compiled
+    fused-quantiser instance (SKINNY_QA).
     Returns C, or (C, q, s) with the codes and scales the kernel used when
     keep_quantized is set."""
     import torch
     m, k = x2.shape
     n = B.shape[0]
+    check_operands(m, n, k, B, None, Bs, bias, out)
     dev = x2.device
     cstruct = _skinny_cached(_freeze(config))
     cus = num_cus(dev)
@@ -330,9 +349,9 @@ def linear_fused(x2, B, Bs, config, eps, bias=None, out=None, keep_quantized=Fal
 def fused_config_ok(entry):
     """True when a table entry can run as the fused-quantiser skinny kernel."""
     c = entry["config"]
-    return (entry["impl"] == "skinny" and int(c.get("BLOCK_T", 0)) == 16
-            and (int(c["BLOCK_W"]) // 16, 1, int(c.get("WAVES_K", 8)), int(c.get("UNROLL", 1)))
-            in SKINNY_QA)
+    return (entry["impl"] == "skinny"
+            and (int(c["BLOCK_W"]) // 16, int(c["BLOCK_T"]) // 16, int(c.get("WAVES_K", 8)),
+                 int(c.get("UNROLL", 1))) in SKINNY_QA)
 
 
 def _freeze(config):
