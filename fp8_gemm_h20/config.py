@@ -33,7 +33,7 @@ from .engine import KERNELS, NATIVE
 _CONFIG_DIR = Path(__file__).with_name("configs")
 _PROFILES = ("35b_tp1", "122b_tp4")
 _POLICIES = ("log_nearest", "nearby_equal_tiles")
-_SPLIT_MODES = ("none", "tail", "full")     # ring and tiled ("last": skinny only)
+_SPLIT_MODES = ("none", "tail", "full")     # ring and tiled ("last": skinny, small-token ring)
 
 
 def available_profiles():
@@ -68,7 +68,9 @@ def _native_ok(impl, c, k):
         kf = c.get("K_FIXED", 0)
         ku = c.get("K_UNROLL", 1)
         split = c.get("SPLIT", 1) if c.get("SPLIT_MODE", "none") != "none" else 1
-        return (c.get("SPLIT_MODE", "none") in _SPLIT_MODES and (kf == 0 or k == 256 * kf // 2) and
+        # SPLIT_MODE "last": the instances with the in-kernel reduction (RING_LAST)
+        modes = _SPLIT_MODES + (("last",) if tt is not None and tt <= 64 and kf == 0 else ())
+        return (c.get("SPLIT_MODE", "none") in modes and (kf == 0 or k == 256 * kf // 2) and
                 (tw, tt, c.get("WAVES_W"), c.get("WAVES_T"), c.get("STAGES"), kf, ku,
                  c.get("WAVES_K", 1)) in RING and
                 (k // 128 // (split if (k // 128) % split == 0 else 1)) % ku == 0)

@@ -524,9 +524,14 @@ constexpr bool ring_has_dp(int TW, int TT, int KF, int KU, int WK) {
     return KU == 1 && WK == 1 && KF == 0 && TW * TT >= 128 * 128;
 }
 
+// Whether a ring instance also has an fp8bg_ring_last kernel (split-K
+// reduced inside the GEMM kernel, FP8BG_SPLIT_LAST): the token tiles of
+// decode and small-M sizes, where few tiles leave most CUs idle.
+constexpr bool ring_has_last(int TT, int KF) { return TT <= 64 && KF == 0; }
+
 // The ring kernel's body.  DPO: every workgroup of the launch is a whole
 // (data-parallel) tile, none computes a K split.
-template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK, bool DPO>
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK, bool DPO, bool LAST>
 __device__ __forceinline__ void ring_body(const KArgs& a) {
     constexpr int NWAVE = WW * WT;                // waves of one K slice
     constexpr int WTW = TW / WW;
@@ -1067,6 +1072,55 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         return;
     }
     if (ks > 0) return;
+    if constexpr (LAST) {
+        // Split-K reduced in this kernel (the reference's last-arriver
+        // reduction, kernels/baseline_gluon.py:194-209), per wave: each wave
+        // stores its WTT x WTW part of the tile's partial with device-scope
+        // stores (coherent across the XCDs' L2s), waits for them, and counts
+        // them in the counter of its part; the wave that completes the count
+        // sums the part over the splits in split order (fp8bg_split_reduce's
+        // order, so C is bitwise the two-kernel result), writes C and resets
+        // the counter.  No wave waits for another and no barrier is needed.
+        const int stile = tile - a.n_dp;
+        const __amdgpu_buffer_rsrc_t wrs =
+            __builtin_amdgcn_make_buffer_rsrc((void*)a.ws, (short)0, 0x7fffffff, kBufferFlags);
+        auto part_off = [&](int sp, int t, int w) -> uint32_t {
+            const int tl = wv_t * WTT + t * 16 + r, wl = wv_w * WTW + w * 16 + qd * 4;
+            return ((uint32_t)(stile * a.split + sp) * (uint32_t)(TW * TT) + (uint32_t)(tl * TW + wl)) * 4u;
+        };
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[w][t]), wrs,
+                                                       part_off(sidx, t, w), 0, kDeviceScope);
+        asm volatile("" ::: "memory");
+        wait_vmcnt<0>();
+        asm volatile("" ::: "memory");
+        uint32_t* cnt = a.cnt + stile * NWAVE + wave;
+        uint32_t arrived = 0;
+        if (lane == 0) arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane(arrived) != (uint32_t)(a.split - 1)) return;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                f32x4 sum = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, part_off(0, t, w), 0, kDeviceScope));
+                for (int sp = 1; sp < a.split; ++sp) {
+                    const f32x4 v = __builtin_bit_cast(
+                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, part_off(sp, t, w), 0, kDeviceScope));
+                    sum[0] += v[0];
+                    sum[1] += v[1];
+                    sum[2] += v[2];
+                    sum[3] += v[3];
+                }
+                const int m = t0 + wv_t * WTT + t * 16 + r, n = w0 + wv_w * WTW + w * 16 + qd * 4;
+                if (m < a.M && n < a.N) *(uint2*)(a.C + (size_t)m * a.N + n) = out_bf16x4(sum, a.bias, n);
+            }
+        if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     float* mine = a.ws + ((size_t)(tile - a.n_dp) * a.split + sidx) * (size_t)(TW * TT);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -1083,7 +1137,17 @@ template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK>
 __global__ __launch_bounds__(64 * WW * WT * WK)
 __attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
 void fp8bg_ring(KArgs a) {
-    ring_body<TW, TT, WW, WT, ST, KF, KU, WK, false>(a);
+    ring_body<TW, TT, WW, WT, ST, KF, KU, WK, false, false>(a);
+}
+
+// The same with the split-K reduction inside the kernel (FP8BG_SPLIT_LAST),
+// for the instances ring_has_last names: a kernel of its own, so that the
+// other launches do not carry its epilogue.
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK>
+__global__ __launch_bounds__(64 * WW * WT * WK)
+__attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
+void fp8bg_ring_last(KArgs a) {
+    ring_body<TW, TT, WW, WT, ST, KF, KU, WK, false, true>(a);
 }
 
 // The same for launches without split tiles: with no epilogue path left
@@ -1093,7 +1157,7 @@ template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK>
 __global__ __launch_bounds__(64 * WW * WT * WK)
 __attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
 void fp8bg_ring_dp(KArgs a) {
-    ring_body<TW, TT, WW, WT, ST, KF, KU, WK, true>(a);
+    ring_body<TW, TT, WW, WT, ST, KF, KU, WK, true, false>(a);
 }
 
 // ===========================================================================
@@ -1111,11 +1175,24 @@ void fp8bg_ring_dp(KArgs a) {
 // (FP8BG_SPLIT_LAST).  The reduction is compiled only into its own instances:
 // its epilogue, even when not taken, costs the common instances registers
 // (skinny<2,1,8,1> 80 -> 86 VGPRs, one workgroup per CU fewer).
-constexpr int kSkinnyQuant = 1, kSkinnyLast = 2;
+// kSkinnyQuantFew: the fused quantiser for launches with at most 4 tokens
+// (16-token tiles, so one token tile).  The general quantiser gives each lane
+// 32 values of one of the tile's 16 tokens: with M = 1 only 4 lanes hold real
+// ones, and every wave of every workgroup runs the full per-value chain.
+// Here the real tokens' 128 values of a group are spread over the whole wave
+// (lane l: token l / 16, values 8 (l % 16) .. + 7); the amax is an unsigned
+// max of the bf16 magnitude bits (exact, and NaN propagates: its magnitude
+// bits exceed infinity's) over the token's 16 lanes by DPP row rotations;
+// the codes go back to the MFMA operand layout through the wave's own slice
+// of the reduction LDS.  Same scales and codes as the general path, so the
+// host may take it for any launch with M <= 4.
+constexpr int kSkinnyQuant = 1, kSkinnyLast = 2, kSkinnyQuantFew = 4;
 template <int NWB, int NTB, int S, int U, int MODE>
 __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     constexpr int TW = 16 * NWB, TT = 16 * NTB, NB = NWB * NTB;
     constexpr bool QA = MODE & kSkinnyQuant, LAST = MODE & kSkinnyLast;
+    constexpr bool QF = MODE & kSkinnyQuantFew;
+    static_assert(!QF || (QA && NTB == 1), "the few-token quantiser takes one 16-token tile");
     __shared__ f32x4 red[S][NB][64];
 
     const int lane = threadIdx.x & 63;
@@ -1155,14 +1232,21 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     const uint16_t* xp[NTB];
 #pragma unroll
     for (int t = 0; t < NTB; ++t) {
-        const int m = min(t0 + 16 * t + r, a.M - 1);
-        if (QA) {
+        // (few-token quantiser: lane l reads token l / 16, values 8 (l % 16) ..)
+        const int m = QF ? min(q, a.M - 1) : min(t0 + 16 * t + r, a.M - 1);
+        if (QF) {
+            xp[t] = a.X + (size_t)m * a.ldx + 8 * r;
+        } else if (QA) {
             xp[t] = a.X + (size_t)m * a.ldx + 32 * q;
         } else {
             tp[t] = a.A + (size_t)m * a.K + 32 * q;
             asp[t] = a.As + (int64_t)m * a.as_sm;
         }
     }
+    // few-token quantiser: the codes of token r of a group, for the lanes of
+    // token r (r < 4), in this wave's slice of the reduction LDS (in order:
+    // a wave's LDS accesses execute in issue order)
+    unsigned char* qstage = (unsigned char*)&red[wave][0][0];
     // side outputs of the fused quantiser come from the first weight tile
     const bool qa_write = QA && a.q_out != nullptr && pw == 0;
 
@@ -1180,7 +1264,7 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     const int J = wave < kcount ? (kcount - 1 - wave) / S + 1 : 0;
     struct Batch {
         i32x8 wv[U][NWB], tv[U][NTB];
-        i32x4 xr[QA ? U : 1][QA ? NTB : 1][4];
+        i32x4 xr[QA ? U : 1][QA ? NTB : 1][QF ? 1 : 4];
         float sa[U][NTB], sb[U][NWB];
     };
     // Loads are issued unconditionally (a group index past the wave's last
@@ -1197,7 +1281,9 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
             }
 #pragma unroll
             for (int t = 0; t < NTB; ++t) {
-                if (QA) {
+                if (QF) {
+                    b.xr[u][t][0] = *(const i32x4*)(xp[t] + (size_t)g * kGroupK);
+                } else if (QA) {
 #pragma unroll
                     for (int c = 0; c < 4; ++c)
                         b.xr[u][t][c] = *(const i32x4*)(xp[t] + (size_t)g * kGroupK + 8 * c);
@@ -1209,7 +1295,62 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
         }
     };
     auto compute = [&](Batch& b, int j0) __attribute__((always_inline)) {
-        if (QA) {
+        if constexpr (QF) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (j0 + u < J) {
+                    const int g = k_lo + wave + S * (j0 + u);
+                    const i32x4 xv = b.xr[u][0][0];
+                    // max of the 8 magnitudes (bf16 bits), then over the
+                    // token's 16 lanes: rotations by 1, 2, 4, 8 in the row
+                    uint32_t mx = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t d = (uint32_t)xv[i] & 0x7fff7fffu;
+                        mx = max(mx, max(d & 0xffffu, d >> 16));
+                    }
+                    mx = max(mx, (uint32_t)__builtin_amdgcn_mov_dpp((int)mx, 0x121, 0xf, 0xf, false));
+                    mx = max(mx, (uint32_t)__builtin_amdgcn_mov_dpp((int)mx, 0x122, 0xf, 0xf, false));
+                    mx = max(mx, (uint32_t)__builtin_amdgcn_mov_dpp((int)mx, 0x124, 0xf, 0xf, false));
+                    mx = max(mx, (uint32_t)__builtin_amdgcn_mov_dpp((int)mx, 0x128, 0xf, 0xf, false));
+                    const bool nan = mx > 0x7f80u;
+                    const float sc = nan ? __builtin_nanf("") : fmaxf(__uint_as_float(mx << 16), a.eps) / 448.0f;
+                    const float rcp = 1.0f / sc;
+                    int o[2];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const uint32_t lo = (uint32_t)xv[2 * i], hi = (uint32_t)xv[2 * i + 1];
+                        int d = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(lo << 16) * rcp,
+                                                                __uint_as_float(lo & 0xffff0000u) * rcp, 0, false);
+                        d = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(hi << 16) * rcp,
+                                                            __uint_as_float(hi & 0xffff0000u) * rcp, d, true);
+                        o[i] = d;
+                    }
+                    asm volatile("" ::: "memory");
+                    *(uint2*)(qstage + q * kGroupK + 8 * r) = make_uint2((uint32_t)o[0], (uint32_t)o[1]);
+                    asm volatile("" ::: "memory");
+                    i32x8 tv = {0, 0, 0, 0, 0, 0, 0, 0};
+                    float sa = 0.f;
+                    // lane (r, q) takes codes 32 q .. 32 q + 31 of token r and
+                    // its scale (held by lanes 16 r .. 16 r + 15)
+                    const float sc_r = __shfl(sc, 16 * (r & 3));
+                    if (r < 4) {
+                        const i32x4 lo = *(const i32x4*)(qstage + r * kGroupK + 32 * q);
+                        const i32x4 hi = *(const i32x4*)(qstage + r * kGroupK + 32 * q + 16);
+                        tv = (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                        sa = sc_r;
+                    }
+                    asm volatile("" ::: "memory");
+                    b.tv[u][0] = tv;
+                    b.sa[u][0] = sa;
+                    if (qa_write && q < a.M) {
+                        uint8_t* qd = a.q_out + (size_t)q * a.K + (size_t)g * kGroupK + 8 * r;
+                        *(uint2*)qd = make_uint2((uint32_t)o[0], (uint32_t)o[1]);
+                        if (r == 0) a.s_out[q * a.qs_sm + g * a.qs_sk] = sc;
+                    }
+                }
+            }
+        } else if (QA) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if (j0 + u < J) {
@@ -1273,7 +1414,7 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     // operand VGPRs of one batch: weights, tokens (and their bf16 source);
     // two batches and the accumulators must leave room for the rest
     // (16 waves per workgroup leave 128 VGPRs per wave, fewer waves 256)
-    constexpr int kBatchRegs = U * (NWB + NTB + (QA ? 2 * NTB : 0)) * 8;
+    constexpr int kBatchRegs = U * (NWB + NTB + (QF ? 1 : QA ? 2 * NTB : 0)) * 8;
     constexpr bool kPipe = 2 * kBatchRegs + 4 * NWB * NTB <= (S >= 16 ? 72 : 160);
     if (J > 0) {
         if constexpr (kPipe) {
@@ -1587,9 +1728,23 @@ FP8BG_TILED(FP8BG_TILED_LAUNCHER)
 FP8BG_SKINNY(FP8BG_SKINNY_LAUNCHER)
 #undef FP8BG_SKINNY_LAUNCHER
 
+// (launches with at most 4 tokens on 16-token tiles take the few-token
+// quantiser: same codes and scales, a fraction of the per-value work)
 #define FP8BG_SKINNY_QA_LAUNCHER(NW, NT, S, U)                                               \
     static void skinny_qa_##NW##_##NT##_##S##_##U(dim3 g, size_t shm, hipStream_t s,        \
                                                   const KArgs& a) {                         \
+        constexpr int kFew = kSkinnyQuant | kSkinnyQuantFew;                                  \
+        if constexpr (NT == 1) {                                                              \
+            if (a.M <= 4) {                                                                   \
+                if (a.split_last)                                                             \
+                    hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kFew | kSkinnyLast>), g,   \
+                                       dim3(64 * S), shm, s, a);                              \
+                else                                                                          \
+                    hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kFew>), g, dim3(64 * S),   \
+                                       shm, s, a);                                            \
+                return;                                                                       \
+            }                                                                                 \
+        }                                                                                     \
         if (a.split_last)                                                                     \
             hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kSkinnyQuant | kSkinnyLast>), g,   \
                                dim3(64 * S), shm, s, a);                                      \
@@ -1603,6 +1758,13 @@ FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_LAUNCHER)
 #define FP8BG_RING_LAUNCHER(TW, TT, WW, WT, ST, KF, KU, WK)                                  \
     static void ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF##_##KU##_##WK(                   \
         dim3 g, size_t shm, hipStream_t s, const KArgs& a) {                                  \
+        if constexpr (ring_has_last(TT, KF)) {                                                 \
+            if (a.split_last) {                                                               \
+                hipLaunchKernelGGL((fp8bg_ring_last<TW, TT, WW, WT, ST, KF, KU, WK>), g,     \
+                                   dim3(64 * WW * WT * WK), shm, s, a);                       \
+                return;                                                                       \
+            }                                                                                 \
+        }                                                                                     \
         if constexpr (ring_has_dp(TW, TT, KF, KU, WK)) {                                      \
             if (a.n_dp == (int)g.x && a.kcount > KU) {                                        \
                 hipLaunchKernelGGL((fp8bg_ring_dp<TW, TT, WW, WT, ST, KF, KU, WK>), g,       \
@@ -1812,7 +1974,7 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     int split = (cfg->split_mode == FP8BG_SPLIT_NONE || k.kf) ? 1 : cfg->split;
     if (kg % split) split = 1;  // reference baseline_gluon.py:274-276
     const bool last = cfg->split_mode == FP8BG_SPLIT_LAST;
-    if (last && !skinny) return FP8BG_ERR_CONFIG;
+    if (last && !skinny && !(ring && ring_has_last(k.tt, k.kf))) return FP8BG_ERR_CONFIG;
     if (skinny && split > 1 && cfg->split_mode == FP8BG_SPLIT_TAIL) return FP8BG_ERR_CONFIG;
     const int64_t tiles_w = (N + k.tw - 1) / k.tw;
     const int64_t tiles_t = ((int64_t)M + k.tt - 1) / k.tt;
@@ -1820,10 +1982,11 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     int64_t n_split = 0;
     if (split > 1) n_split = cfg->split_mode == FP8BG_SPLIT_TAIL ? tiles % num_cus : tiles;
     if (n_split == 0) split = 1;
-    // the in-kernel reduction: one counter per split tile, partial byte
-    // offsets below 2^31
+    // the in-kernel reduction: one counter per split tile (skinny) or per
+    // wave of a split tile (ring), partial byte offsets below 2^31
     if (last && split > 1 &&
-        (n_split > FP8BG_COUNTERS || n_split * split * (int64_t)k.tw * k.tt * 4 > 0x7fffffffLL))
+        (n_split * (ring ? k.ww * k.wt : 1) > FP8BG_COUNTERS ||
+         n_split * split * (int64_t)k.tw * k.tt * 4 > 0x7fffffffLL))
         return FP8BG_ERR_SHAPE;
     // a ring kernel computing KU groups per barrier needs whole multiples of
     // KU in every workgroup's K range (kg / split divides kg)

@@ -105,6 +105,10 @@ RING = (
     # 64x64 with 2x2 waves (two weight blocks per wave)
     (64, 64, 2, 2, 8, 0, 4, 1),
 )
+# ring instances with the in-kernel split-K reduction (fp8bg_ring_last,
+# SPLIT_MODE "last"): token tiles up to 64, no fixed K; must match
+# ring_has_last in csrc/fp8bg.hip
+RING_LAST = tuple(c for c in RING if c[1] <= 64 and c[5] == 0)
 SPLIT_MODES = {"none": _lib.SPLIT_NONE, "tail": _lib.SPLIT_TAIL, "full": _lib.SPLIT_FULL,
                "last": _lib.SPLIT_LAST}
 

@@ -69,7 +69,7 @@ extern "C" {
 #define FP8BG_SPLIT_NONE 0
 /* Tail split (reference kernels/baseline_gluon.py:274-287): the first
  * tiles - (tiles % num_cus) tiles run whole; only the last partial wave is
- * split over `split` workgroups.  Tiled kernel only. */
+ * split over `split` workgroups.  Tiled and ring kernels. */
 #define FP8BG_SPLIT_TAIL 1
 /* Full split (reference kernels/baseline_triton.py:100-114): every tile is
  * split. */
@@ -77,13 +77,15 @@ extern "C" {
 /* In both split modes the fp32 partials go to the caller's workspace and a
  * second kernel on the same stream sums them in fixed split order and writes
  * bf16 (deterministic, replay-safe, no atomics or counters). */
-/* Full split reduced inside the GEMM kernel (skinny kernel only): each
- * workgroup writes its partial tile with device-scope stores and counts it in
- * the tile's counter; the workgroup that completes the count sums the
- * partials in split order (bitwise the FP8BG_SPLIT_FULL result), writes C and
- * resets the counter.  One launch instead of two (the reference's
- * self-resetting counters, kernels/baseline_gluon.py:194-209, with the
- * summation order fixed).  At most FP8BG_COUNTERS split tiles. */
+/* Full split reduced inside the GEMM kernel: skinny kernels, and ring
+ * kernels with block_t <= 64 and k_fixed 0.  Each split workgroup (skinny),
+ * or each wave's part of a split tile (ring), writes its partial with
+ * device-scope stores and counts it in its counter; the one that completes
+ * the count sums the partials in split order (bitwise the FP8BG_SPLIT_FULL
+ * result), writes C and resets the counter.  One launch instead of two (the
+ * reference's self-resetting counters, kernels/baseline_gluon.py:194-209,
+ * with the summation order fixed).  At most FP8BG_COUNTERS counters: split
+ * tiles (skinny) or split tiles x waves_w x waves_t (ring). */
 #define FP8BG_SPLIT_LAST 3
 
 /* Split-K workspace layout (every split mode): FP8BG_COUNTERS uint32 tile

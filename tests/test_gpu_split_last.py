@@ -1,4 +1,4 @@
-"""The skinny kernel's in-kernel split-K reduction (SPLIT_MODE "last").
+"""The in-kernel split-K reduction (SPLIT_MODE "last") of the skinny and ring kernels.
 
 Each split workgroup stores its partial tile with device-scope stores and
 counts it in the tile's counter; the workgroup that completes the count sums
@@ -127,3 +127,67 @@ def test_in_kernel_split_fused_quantiser_and_no_alloc():
                                           _lib.num_cus(0), torch.cuda.current_stream().cuda_stream))
         torch.cuda.synchronize()
         assert torch.equal(C.view(torch.int16), want.view(torch.int16))
+
+
+# ring instances with token tiles up to 64 (fp8bg_ring_last): each wave of a
+# split tile counts its own part, the last one sums it in split order
+RING_CASES = [
+    (37, 3072, 2048, dict(BLOCK_W=64, BLOCK_T=64, WAVES_W=4, WAVES_T=1, STAGES=4, SPLIT=4)),
+    (64, 4608, 3072, dict(BLOCK_W=64, BLOCK_T=64, WAVES_W=4, WAVES_T=1, STAGES=8, K_UNROLL=4, WAVES_K=2,
+                          SPLIT=2)),
+    (32, 12288, 2048, dict(BLOCK_W=128, BLOCK_T=32, WAVES_W=4, WAVES_T=1, STAGES=4, SPLIT=2)),
+    (50, 512, 3072, dict(BLOCK_W=64, BLOCK_T=64, WAVES_W=2, WAVES_T=2, STAGES=8, K_UNROLL=4, SPLIT=2)),
+    (100, 3072, 2048, dict(BLOCK_W=192, BLOCK_T=64, WAVES_W=6, WAVES_T=2, STAGES=4, SPLIT=2)),
+    (37, 2048, 4096, dict(BLOCK_W=64, BLOCK_T=64, WAVES_W=4, WAVES_T=1, STAGES=8, K_UNROLL=4, WAVES_K=4,
+                          SPLIT=2)),
+    (7, 1024, 2048, dict(BLOCK_W=128, BLOCK_T=64, WAVES_W=4, WAVES_T=1, STAGES=6, K_UNROLL=2, WAVES_K=2,
+                         SPLIT=4, XCD_REMAP=True)),
+]
+
+
+@pytest.mark.parametrize("m,n,k,cfg", RING_CASES, ids=lambda v: str(v) if not isinstance(v, dict) else "")
+def test_ring_in_kernel_split_is_bitwise_the_two_kernel_split(m, n, k, cfg):
+    print(f"ring split last M={m} N={n} K={k} {cfg}", flush=True)
+    last = dict(cfg, SPLIT_MODE="last")
+    full = dict(cfg, SPLIT_MODE="full")
+    inputs = [quant.make_inputs(m, n, k, seed=s, device="cuda") for s in (5, 6)]
+    bias = torch.randn(n, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16).cuda()
+    want = [kernels.ring(*x, full) for x in inputs]
+    want_b = [kernels.ring(*x, full, bias=bias) for x in inputs]
+    for x, w in zip(inputs, want):
+        check(w, oracle_ref(*x), (m, n, k, "ring full"))
+    for i in range(16):
+        j = i % 2
+        got = kernels.ring(*inputs[j], last)
+        assert torch.equal(got.view(torch.int16), want[j].view(torch.int16)), (i, m, n, k)
+        if i % 3 == 0:
+            assert torch.equal(kernels.ring(*inputs[j], full), want[j])
+        if i % 4 == 1:
+            got_b = kernels.ring(*inputs[j], last, bias=bias)
+            assert torch.equal(got_b.view(torch.int16), want_b[j].view(torch.int16)), (i, "bias")
+    torch.cuda.synchronize()
+
+
+def test_ring_in_kernel_split_graph_replays():
+    m, n, k = 37, 3072, 2048
+    cfg = dict(BLOCK_W=64, BLOCK_T=64, WAVES_W=4, WAVES_T=1, STAGES=8, K_UNROLL=4, WAVES_K=2, SPLIT=4,
+               SPLIT_MODE="last")
+    args = quant.make_inputs(m, n, k, seed=9, device="cuda")
+    eager = kernels.ring(*args, dict(cfg, SPLIT_MODE="full"))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            kernels.ring(*args, cfg)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        outs = [kernels.ring(*args, cfg) for _ in range(6)]
+    for r in range(20):
+        with torch.cuda.stream(s):
+            g.replay()
+        if r % 5 == 4:
+            torch.cuda.synchronize()
+            for o in outs:
+                assert torch.equal(o.view(torch.int16), eager.view(torch.int16)), r
+    torch.cuda.synchronize()
