@@ -57,6 +57,7 @@ EXPORTS = (
     "fp8bg_calib_mfma",
     "fp8bg_calib_read",
     "fp8bg_calib_write",
+    "fp8bg_calib_launch",
     "fp8bg_strerror",
 )
 
@@ -154,6 +155,8 @@ def _declare(lib):
     lib.fp8bg_calib_read.restype = ctypes.c_int
     lib.fp8bg_calib_write.argtypes = [vp, i64, ctypes.c_uint32, i32, i32, vp]
     lib.fp8bg_calib_write.restype = ctypes.c_int
+    lib.fp8bg_calib_launch.argtypes = [i32, vp]
+    lib.fp8bg_calib_launch.restype = ctypes.c_int
     lib.fp8bg_strerror.argtypes = [ctypes.c_int]
     lib.fp8bg_strerror.restype = ctypes.c_char_p
 

@@ -301,6 +301,10 @@ int fp8bg_e4m3_encode_host(const float* x, uint8_t* out, int64_t n);
  * with the 32-bit `value`, `workgroups` workgroups of 256 threads issuing
  * 16-byte stores; nontemporal != 0 uses the non-temporal stores the GEMM
  * kernels write C with.
+ *
+ * fp8bg_calib_launch: an empty kernel of `workgroups` workgroups of 64
+ * threads; back to back in a hipGraph, its time per launch is the launch
+ * floor of every call.
  */
 #define FP8BG_CALIB_MAX_ITERS 8192
 int fp8bg_calib_mfma(const int32_t* codes, float* out, int32_t workgroups, int32_t iters,
@@ -309,6 +313,7 @@ int fp8bg_calib_read(const void* src, int64_t bytes, uint32_t* out, int32_t work
                      void* stream);
 int fp8bg_calib_write(void* dst, int64_t bytes, uint32_t value, int32_t workgroups, int32_t nontemporal,
                       void* stream);
+int fp8bg_calib_launch(int32_t workgroups, void* stream);
 
 /* Static message for an error code. */
 const char* fp8bg_strerror(int code);
