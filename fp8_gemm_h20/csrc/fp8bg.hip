@@ -1219,28 +1219,42 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     const int w0 = pw * TW, t0 = pt * TT;
     const int k_lo = sidx * kcount;
 
+    // Operand loads are coalesced: lane l reads row l >> 2 of a 16-row block,
+    // 16-byte chunks (l & 3) and 4 + (l & 3) of the 128-byte group, so a quad
+    // of lanes reads 64 contiguous bytes of ONE row (one L1 access; a quad
+    // spread over four rows costs four, and the L1's access rate, not HBM,
+    // then bounds the kernel).  ds_bpermute hands MFMA lane (r, q) the data
+    // of loading lane 4 r + q: row r, chunks q and 4 + q (K bytes [16 q, +16)
+    // and [64 + 16 q, +16)).  Weights and tokens use this one byte -> K
+    // assignment, so each MFMA still reduces exactly its group's 128 products.
+    const int lr = lane >> 2, lc = lane & 3;
+    const int op_src = (4 * r + q) << 2;
+    // The Bs block of the whole tile (TW divides 128, so the tile's rows
+    // share one) and the As rows, read with one load per batch: lane l takes
+    // group slot u of token row l >> 2 (row-major As: a quad reads 4 nearby
+    // floats of one row) or u = l >> 4 of row l & 15 (column-major As), and
+    // lane (r, q) gets its row's scale of slot u by ds_bpermute.
+    static_assert(128 % TW == 0, "a skinny tile lies inside one 128-row Bs block");
+    const bool as_cm = a.as_sm == 1;
+    const int sa_row = as_cm ? (lane & 15) : lr, sa_u = as_cm ? (lane >> 4) : lc;
+    const float* bsp = a.Bs + (int64_t)(w0 >> 7) * a.bs_sn;
     const uint8_t* wp[NWB];
-    const float* bsp[NWB];
 #pragma unroll
-    for (int w = 0; w < NWB; ++w) {
-        const int n = min(w0 + 16 * w + r, a.N - 1);
-        wp[w] = a.B + (size_t)n * a.K + 32 * q;
-        bsp[w] = a.Bs + (int64_t)(min(w0 + 16 * w, a.N - 1) >> 7) * a.bs_sn;
-    }
+    for (int w = 0; w < NWB; ++w) wp[w] = a.B + (size_t)min(w0 + 16 * w + lr, a.N - 1) * a.K + 16 * lc;
     const uint8_t* tp[NTB];
     const float* asp[NTB];
     const uint16_t* xp[NTB];
 #pragma unroll
     for (int t = 0; t < NTB; ++t) {
-        // (few-token quantiser: lane l reads token l / 16, values 8 (l % 16) ..)
-        const int m = QF ? min(q, a.M - 1) : min(t0 + 16 * t + r, a.M - 1);
         if (QF) {
-            xp[t] = a.X + (size_t)m * a.ldx + 8 * r;
+            // few-token quantiser: lane l reads token l / 16, values 8 (l % 16) ..
+            xp[t] = a.X + (size_t)min(q, a.M - 1) * a.ldx + 8 * r;
         } else if (QA) {
-            xp[t] = a.X + (size_t)m * a.ldx + 32 * q;
+            // lane (r, q): token r, values [16 q, +16) and [64 + 16 q, +16)
+            xp[t] = a.X + (size_t)min(t0 + 16 * t + r, a.M - 1) * a.ldx + 16 * q;
         } else {
-            tp[t] = a.A + (size_t)m * a.K + 32 * q;
-            asp[t] = a.As + (int64_t)m * a.as_sm;
+            tp[t] = a.A + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.K + 16 * lc;
+            asp[t] = a.As + (int64_t)min(t0 + 16 * t + sa_row, a.M - 1) * a.as_sm;
         }
     }
     // few-token quantiser: the codes of token r of a group, for the lanes of
@@ -1263,36 +1277,54 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     // (the accumulation order, and so the result, is the same either way).
     const int J = wave < kcount ? (kcount - 1 - wave) / S + 1 : 0;
     struct Batch {
-        i32x8 wv[U][NWB], tv[U][NTB];
+        i32x4 wl[U][NWB][2], tl[QA ? 1 : U][QA ? 1 : NTB][2];   // as loaded (coalesced)
+        i32x8 tv[U][NTB];                                       // quantised tokens (QA)
         i32x4 xr[QA ? U : 1][QA ? NTB : 1][QF ? 1 : 4];
-        float sa[U][NTB], sb[U][NWB];
+        float sa[U][NTB];                                       // token scales (QA)
+        float sar[NTB], sbr;                                    // lane-indexed scales
     };
     // Loads are issued unconditionally (a group index past the wave's last
     // group is clamped to it; compute skips those), so they form straight-
     // line code and each batch's computation waits only for its own loads.
+    auto group = [&](int j) __attribute__((always_inline)) { return k_lo + wave + S * min(j, J - 1); };
     auto load = [&](Batch& b, int j0) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int g = k_lo + wave + S * min(j0 + u, J - 1);
+            const size_t go = (size_t)group(j0 + u) * kGroupK;
 #pragma unroll
             for (int w = 0; w < NWB; ++w) {
-                b.wv[u][w] = load_op(wp[w] + (size_t)g * kGroupK);
-                b.sb[u][w] = bsp[w][(int64_t)g * a.bs_sk];
+                b.wl[u][w][0] = *(const i32x4*)(wp[w] + go);
+                b.wl[u][w][1] = *(const i32x4*)(wp[w] + go + 64);
             }
 #pragma unroll
             for (int t = 0; t < NTB; ++t) {
                 if (QF) {
-                    b.xr[u][t][0] = *(const i32x4*)(xp[t] + (size_t)g * kGroupK);
+                    b.xr[u][t][0] = *(const i32x4*)(xp[t] + go);
                 } else if (QA) {
 #pragma unroll
                     for (int c = 0; c < 4; ++c)
-                        b.xr[u][t][c] = *(const i32x4*)(xp[t] + (size_t)g * kGroupK + 8 * c);
+                        b.xr[u][t][c] = *(const i32x4*)(xp[t] + go + 8 * (c & 1) + 64 * (c >> 1));
                 } else {
-                    b.tv[u][t] = load_op(tp[t] + (size_t)g * kGroupK);
-                    b.sa[u][t] = asp[t][(int64_t)g * a.as_sk];
+                    b.tl[u][t][0] = *(const i32x4*)(tp[t] + go);
+                    b.tl[u][t][1] = *(const i32x4*)(tp[t] + go + 64);
                 }
             }
         }
+        b.sbr = bsp[(int64_t)group(j0 + min(lane, U - 1)) * a.bs_sk];
+        if (!QA) {
+#pragma unroll
+            for (int t = 0; t < NTB; ++t) b.sar[t] = asp[t][(int64_t)group(j0 + min(sa_u, U - 1)) * a.as_sk];
+        }
+    };
+    // MFMA operand of lane (r, q) from the coalesced loads of a 16-row block
+    auto gather = [&](const i32x4 (&v)[2]) __attribute__((always_inline)) {
+        i32x8 o;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            o[d] = __builtin_amdgcn_ds_bpermute(op_src, v[0][d]);
+            o[4 + d] = __builtin_amdgcn_ds_bpermute(op_src, v[1][d]);
+        }
+        return o;
     };
     auto compute = [&](Batch& b, int j0) __attribute__((always_inline)) {
         if constexpr (QF) {
@@ -1331,12 +1363,12 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                     asm volatile("" ::: "memory");
                     i32x8 tv = {0, 0, 0, 0, 0, 0, 0, 0};
                     float sa = 0.f;
-                    // lane (r, q) takes codes 32 q .. 32 q + 31 of token r and
-                    // its scale (held by lanes 16 r .. 16 r + 15)
+                    // lane (r, q) takes codes [16 q, +16) and [64 + 16 q, +16)
+                    // of token r and its scale (held by lanes 16 r .. 16 r + 15)
                     const float sc_r = __shfl(sc, 16 * (r & 3));
                     if (r < 4) {
-                        const i32x4 lo = *(const i32x4*)(qstage + r * kGroupK + 32 * q);
-                        const i32x4 hi = *(const i32x4*)(qstage + r * kGroupK + 32 * q + 16);
+                        const i32x4 lo = *(const i32x4*)(qstage + r * kGroupK + 16 * q);
+                        const i32x4 hi = *(const i32x4*)(qstage + r * kGroupK + 64 + 16 * q);
                         tv = (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                         sa = sc_r;
                     }
@@ -1391,9 +1423,9 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                         b.sa[u][t] = sc;
                         const int m = t0 + 16 * t + r;
                         if (qa_write && m < a.M) {
-                            uint8_t* qd = a.q_out + (size_t)m * a.K + (size_t)g * kGroupK + 32 * q;
+                            uint8_t* qd = a.q_out + (size_t)m * a.K + (size_t)g * kGroupK + 16 * q;
                             *(i32x4*)qd = (i32x4){o[0], o[1], o[2], o[3]};
-                            *(i32x4*)(qd + 16) = (i32x4){o[4], o[5], o[6], o[7]};
+                            *(i32x4*)(qd + 64) = (i32x4){o[4], o[5], o[6], o[7]};
                             if (q == 0) a.s_out[m * a.qs_sm + g * a.qs_sk] = sc;
                         }
                     }
@@ -1403,11 +1435,26 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (j0 + u < J) {
+                const float sb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b.sbr), u));
+                i32x8 tv[NTB];
+                float sa[NTB];
 #pragma unroll
-                for (int w = 0; w < NWB; ++w)
+                for (int t = 0; t < NTB; ++t) {
+                    if constexpr (QA) {
+                        tv[t] = b.tv[u][t];
+                        sa[t] = b.sa[u][t];
+                    } else {
+                        tv[t] = gather(b.tl[u][t]);
+                        const int src = as_cm ? r + 16 * u : 4 * r + u;
+                        sa[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(b.sar[t])));
+                    }
+                }
 #pragma unroll
-                    for (int t = 0; t < NTB; ++t)
-                        promote(acc[w][t], mfma16x16x128(b.wv[u][w], b.tv[u][t]), b.sa[u][t] * b.sb[u][w]);
+                for (int w = 0; w < NWB; ++w) {
+                    const i32x8 wv = gather(b.wl[u][w]);
+#pragma unroll
+                    for (int t = 0; t < NTB; ++t) promote(acc[w][t], mfma16x16x128(wv, tv[t]), sa[t] * sb);
+                }
             }
         }
     };
