@@ -16,9 +16,12 @@
 // is ONE fp32 scalar per lane per 16x16 block and group.
 //
 // Operand layout in a lane (both operands identical): row (lane & 15) of a
-// 16-row block, bytes [32 * (lane >> 4), +32) of the 128-byte group.  Since A
-// and B use the same byte -> K assignment, the MFMA reduction covers exactly
-// the 128 products of the group whatever order the hardware sums them in.
+// 16-row block, bytes [32 * (lane >> 4), +32) of the 128-byte group (LDS-fed
+// kernels), or bytes [16 * (lane >> 4), +16) and [64 + 16 * (lane >> 4), +16)
+// (fp8bg_skinny, whose operands arrive by coalesced loads and ds_bpermute).
+// Since A and B use the same byte -> K assignment, the MFMA reduction covers
+// exactly the 128 products of the group whatever order the hardware sums them
+// in.
 //
 // Kernels:
 //  * fp8bg_tiled  - LDS-tiled workgroup tile (weights x tokens), 4 waves, a
@@ -1250,8 +1253,9 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
             // few-token quantiser: lane l reads token l / 16, values 8 (l % 16) ..
             xp[t] = a.X + (size_t)min(q, a.M - 1) * a.ldx + 8 * r;
         } else if (QA) {
-            // lane (r, q): token r, values [16 q, +16) and [64 + 16 q, +16)
-            xp[t] = a.X + (size_t)min(t0 + 16 * t + r, a.M - 1) * a.ldx + 16 * q;
+            // loading lane l: token l >> 2, values [16 (l & 3), +16) and
+            // [64 + 16 (l & 3), +16) (a quad holds the token's whole group)
+            xp[t] = a.X + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.ldx + 16 * lc;
         } else {
             tp[t] = a.A + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.K + 16 * lc;
             asp[t] = a.As + (int64_t)min(t0 + 16 * t + sa_row, a.M - 1) * a.as_sm;
@@ -1397,20 +1401,22 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                                 v[8 * c + 2 * i] = __uint_as_float((uint32_t)b.xr[u][t][c][i] << 16);
                                 v[8 * c + 2 * i + 1] = __uint_as_float((uint32_t)b.xr[u][t][c][i] & 0xffff0000u);
                             }
-                        float amax = 0.f;
-                        bool nan = false;
+                        // the quad of lanes 4 lr .. 4 lr + 3 holds token lr's
+                        // group: amax as an unsigned max of the bf16 magnitude
+                        // bits (exact; a NaN's exceed infinity's), over the
+                        // quad by two DPP quad permutations
+                        uint32_t mx = 0;
 #pragma unroll
-                        for (int i = 0; i < 32; ++i) {
-                            amax = fmaxf(amax, fabsf(v[i]));
-                            nan |= __builtin_isnan(v[i]);
-                        }
-                        // lanes r, r + 16, r + 32, r + 48 hold the token's group
+                        for (int c = 0; c < 4; ++c)
 #pragma unroll
-                        for (int d = 16; d < 64; d <<= 1) {
-                            amax = fmaxf(amax, __shfl_xor(amax, d));
-                            nan |= __shfl_xor((int)nan, d) != 0;
-                        }
-                        const float sc = nan ? __builtin_nanf("") : fmaxf(amax, a.eps) / 448.0f;
+                            for (int i = 0; i < 4; ++i) {
+                                const uint32_t d = (uint32_t)b.xr[u][t][c][i] & 0x7fff7fffu;
+                                mx = max(mx, max(d & 0xffffu, d >> 16));
+                            }
+                        mx = max(mx, (uint32_t)__builtin_amdgcn_mov_dpp((int)mx, 0xb1, 0xf, 0xf, false));
+                        mx = max(mx, (uint32_t)__builtin_amdgcn_mov_dpp((int)mx, 0x4e, 0xf, 0xf, false));
+                        const bool nan = mx > 0x7f80u;
+                        const float sc = nan ? __builtin_nanf("") : fmaxf(__uint_as_float(mx << 16), a.eps) / 448.0f;
                         const float rcp = 1.0f / sc;
                         i32x8 o;
 #pragma unroll
@@ -1419,14 +1425,16 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                             d = __builtin_amdgcn_cvt_pk_fp8_f32(v[4 * i + 2] * rcp, v[4 * i + 3] * rcp, d, true);
                             o[i] = d;
                         }
+                        // codes and scale in the loading layout (gathered
+                        // into the MFMA layout with the weights)
                         b.tv[u][t] = o;
                         b.sa[u][t] = sc;
-                        const int m = t0 + 16 * t + r;
+                        const int m = t0 + 16 * t + lr;
                         if (qa_write && m < a.M) {
-                            uint8_t* qd = a.q_out + (size_t)m * a.K + (size_t)g * kGroupK + 16 * q;
+                            uint8_t* qd = a.q_out + (size_t)m * a.K + (size_t)g * kGroupK + 16 * lc;
                             *(i32x4*)qd = (i32x4){o[0], o[1], o[2], o[3]};
                             *(i32x4*)(qd + 64) = (i32x4){o[4], o[5], o[6], o[7]};
-                            if (q == 0) a.s_out[m * a.qs_sm + g * a.qs_sk] = sc;
+                            if (lc == 0) a.s_out[m * a.qs_sm + g * a.qs_sk] = sc;
                         }
                     }
                 }
@@ -1440,9 +1448,13 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                 float sa[NTB];
 #pragma unroll
                 for (int t = 0; t < NTB; ++t) {
-                    if constexpr (QA) {
+                    if constexpr (QF) {
                         tv[t] = b.tv[u][t];
                         sa[t] = b.sa[u][t];
+                    } else if constexpr (QA) {
+                        const i32x8 o = b.tv[u][t];
+                        tv[t] = gather({(i32x4){o[0], o[1], o[2], o[3]}, (i32x4){o[4], o[5], o[6], o[7]}});
+                        sa[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(op_src, __float_as_int(b.sa[u][t])));
                     } else {
                         tv[t] = gather(b.tl[u][t]);
                         const int src = as_cm ? r + 16 * u : 4 * r + u;
