@@ -2046,11 +2046,13 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     if (split > 1) n_split = cfg->split_mode == FP8BG_SPLIT_TAIL ? tiles % num_cus : tiles;
     if (n_split == 0) split = 1;
     // the in-kernel reduction: one counter per split tile (skinny) or per
-    // wave of a split tile (ring), partial byte offsets below 2^31
-    if (last && split > 1 &&
-        (n_split * (ring ? k.ww * k.wt : 1) > FP8BG_COUNTERS ||
-         n_split * split * (int64_t)k.tw * k.tt * 4 > 0x7fffffffLL))
-        return FP8BG_ERR_SHAPE;
+    // wave of a split tile (ring), partial byte offsets below 2^31; beyond
+    // that the split tiles take the two-kernel reduction, which sums the same
+    // partials in the same order (bitwise the same C), so a table entry of
+    // this mode stays valid at any M
+    const bool in_kernel = last && n_split > 0 &&
+                           n_split * (ring ? k.ww * k.wt : 1) <= FP8BG_COUNTERS &&
+                           n_split * split * (int64_t)k.tw * k.tt * 4 <= 0x7fffffffLL;
     // a ring kernel computing KU groups per barrier needs whole multiples of
     // KU in every workgroup's K range (kg / split divides kg)
     if (ring && (kg / split) % k.unroll) return FP8BG_ERR_CONFIG;
@@ -2077,7 +2079,7 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     plan->n_dp = (int32_t)n_dp;
     plan->n_split = (int32_t)n_split;
     plan->grid = (int32_t)grid;
-    plan->launches = n_split && !last ? 2 : 1;
+    plan->launches = n_split && !in_kernel ? 2 : 1;
     plan->ws_elems = n_split ? FP8BG_COUNTERS + n_split * split * (int64_t)k.tw * k.tt : 0;
     plan->lds_bytes = (int32_t)lds;
     plan->threads = k.threads;
@@ -2121,7 +2123,7 @@ int gemm_enqueue(const void* A, const void* B, const float* As, int64_t as_strid
     // workspace: the tile counters, then the partials
     a.cnt = (uint32_t*)ws;
     a.ws = ws ? ws + FP8BG_COUNTERS : nullptr;
-    a.split_last = cfg->split_mode == FP8BG_SPLIT_LAST && p.n_split > 0;
+    a.split_last = p.n_split > 0 && p.launches == 1;  // FP8BG_SPLIT_LAST within its limits
     a.as_sm = as_stride_m;
     a.as_sk = as_stride_k;
     a.bs_sn = bs_stride_n;
@@ -2251,7 +2253,7 @@ int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps, const void* B
     a.bias = (const uint16_t*)bias;
     a.cnt = (uint32_t*)ws;
     a.ws = ws ? ws + FP8BG_COUNTERS : nullptr;
-    a.split_last = cfg->split_mode == FP8BG_SPLIT_LAST && p.n_split > 0;
+    a.split_last = p.n_split > 0 && p.launches == 1;  // FP8BG_SPLIT_LAST within its limits
     a.bs_sn = bs_stride_n;
     a.bs_sk = bs_stride_k;
     a.M = M;

@@ -85,7 +85,9 @@ extern "C" {
  * result), writes C and resets the counter.  One launch instead of two (the
  * reference's self-resetting counters, kernels/baseline_gluon.py:194-209,
  * with the summation order fixed).  At most FP8BG_COUNTERS counters: split
- * tiles (skinny) or split tiles x waves_w x waves_t (ring). */
+ * tiles (skinny) or split tiles x waves_w x waves_t (ring), and partials
+ * below 2^31 bytes; a launch beyond either limit takes the FP8BG_SPLIT_FULL
+ * reduction instead (plan.launches = 2, the same C bit for bit). */
 #define FP8BG_SPLIT_LAST 3
 
 /* Split-K workspace layout (every split mode): FP8BG_COUNTERS uint32 tile

@@ -191,3 +191,21 @@ def test_ring_in_kernel_split_graph_replays():
             for o in outs:
                 assert torch.equal(o.view(torch.int16), eager.view(torch.int16)), r
     torch.cuda.synchronize()
+
+
+def test_in_kernel_split_beyond_the_counters_takes_two_launches():
+    # 384 split tiles of 192 x 64 with 12 waves need 4608 counters, more than
+    # FP8BG_COUNTERS: the plan falls back to the two-kernel reduction, and the
+    # entry still gives the full split's C bit for bit (a table entry of this
+    # mode tuned at a smaller M stays usable at any M)
+    m, n, k = 384, 12288, 2048
+    cfg = dict(BLOCK_W=192, BLOCK_T=64, WAVES_W=6, WAVES_T=2, STAGES=4, SPLIT=2)
+    plan = _lib.make_plan(m, n, k, kernels.ring_struct(dict(cfg, SPLIT_MODE="last")), 256)
+    assert (plan.n_split, plan.launches) == (384, 2)
+    print(f"ring split last beyond counters M={m} N={n} K={k}", flush=True)
+    args = quant.make_inputs(m, n, k, seed=3, device="cuda")
+    want = kernels.ring(*args, dict(cfg, SPLIT_MODE="full"))
+    check(want, oracle_ref(*args), "ring full, 384 split tiles")
+    got = kernels.ring(*args, dict(cfg, SPLIT_MODE="last"))
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    torch.cuda.synchronize()
