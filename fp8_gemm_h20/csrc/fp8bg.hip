@@ -1167,8 +1167,8 @@ void fp8bg_ring_dp(KArgs a) {
 // Small-M kernel: operands straight from global memory, waves split K
 // ===========================================================================
 // With QA the token operand is quantised in registers from bf16 activations:
-// the four lanes holding one token's 128-K group reduce its amax by lane
-// shuffles, s = max(amax, eps) / 448 and each value becomes
+// the quad of lanes holding one token's 128-K group reduces its amax by two
+// DPP permutations, s = max(amax, eps) / 448 and each value becomes
 // e4m3(x * (1 / s)) through v_cvt_pk_fp8_f32 (round to nearest even; the
 // same code as the integer encoder for every non-NaN input).  The
 // reciprocal replaces the standalone quantiser's division: one multiply per
@@ -1189,13 +1189,22 @@ void fp8bg_ring_dp(KArgs a) {
 // the codes go back to the MFMA operand layout through the wave's own slice
 // of the reduction LDS.  Same scales and codes as the general path, so the
 // host may take it for any launch with M <= 4.
-constexpr int kSkinnyQuant = 1, kSkinnyLast = 2, kSkinnyQuantFew = 4;
+// kSkinnyFewTokens: fp8 tokens for launches with at most 8 of them.  Rows of
+// the 16-token operand at or past M feed only outputs that are never stored,
+// so one 16-byte load per lane covers the group of rows 0..7 (lane l: row
+// l >> 3, chunk l & 7): half the L1 accesses of the two loads that cover 16
+// rows, which at M <= 8 cost as much as the weights' own loads.  The same
+// eight ds_bpermute passes give MFMA lane (r, q) chunks q and 4 + q of row
+// r & 7; bitwise the same C as the general path.
+constexpr int kSkinnyQuant = 1, kSkinnyLast = 2, kSkinnyQuantFew = 4, kSkinnyFewTokens = 8;
 template <int NWB, int NTB, int S, int U, int MODE>
 __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     constexpr int TW = 16 * NWB, TT = 16 * NTB, NB = NWB * NTB;
     constexpr bool QA = MODE & kSkinnyQuant, LAST = MODE & kSkinnyLast;
     constexpr bool QF = MODE & kSkinnyQuantFew;
+    constexpr bool FT = MODE & kSkinnyFewTokens;
     static_assert(!QF || (QA && NTB == 1), "the few-token quantiser takes one 16-token tile");
+    static_assert(!FT || (!QA && NTB == 1), "the few-token load takes one 16-token tile of fp8 tokens");
     __shared__ f32x4 red[S][NB][64];
 
     const int lane = threadIdx.x & 63;
@@ -1257,7 +1266,8 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
             // [64 + 16 (l & 3), +16) (a quad holds the token's whole group)
             xp[t] = a.X + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.ldx + 16 * lc;
         } else {
-            tp[t] = a.A + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.K + 16 * lc;
+            tp[t] = FT ? a.A + (size_t)min(t0 + (lane >> 3), a.M - 1) * a.K + 16 * (lane & 7)
+                       : a.A + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.K + 16 * lc;
             asp[t] = a.As + (int64_t)min(t0 + 16 * t + sa_row, a.M - 1) * a.as_sm;
         }
     }
@@ -1310,7 +1320,7 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                         b.xr[u][t][c] = *(const i32x4*)(xp[t] + go + 8 * (c & 1) + 64 * (c >> 1));
                 } else {
                     b.tl[u][t][0] = *(const i32x4*)(tp[t] + go);
-                    b.tl[u][t][1] = *(const i32x4*)(tp[t] + go + 64);
+                    if (!FT) b.tl[u][t][1] = *(const i32x4*)(tp[t] + go + 64);
                 }
             }
         }
@@ -1321,6 +1331,18 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
         }
     };
     // MFMA operand of lane (r, q) from the coalesced loads of a 16-row block
+    // (few-token load: chunk q of row r & 7 sits in loading lane 8 (r & 7) + q,
+    // chunk 4 + q in lane 8 (r & 7) + 4 + q)
+    const int few_src = (8 * (r & 7) + q) << 2;
+    auto gather_few = [&](const i32x4& v) __attribute__((always_inline)) {
+        i32x8 o;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            o[d] = __builtin_amdgcn_ds_bpermute(few_src, v[d]);
+            o[4 + d] = __builtin_amdgcn_ds_bpermute(few_src + 16, v[d]);
+        }
+        return o;
+    };
     auto gather = [&](const i32x4 (&v)[2]) __attribute__((always_inline)) {
         i32x8 o;
 #pragma unroll
@@ -1456,7 +1478,7 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                         tv[t] = gather({(i32x4){o[0], o[1], o[2], o[3]}, (i32x4){o[4], o[5], o[6], o[7]}});
                         sa[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(op_src, __float_as_int(b.sa[u][t])));
                     } else {
-                        tv[t] = gather(b.tl[u][t]);
+                        tv[t] = FT ? gather_few(b.tl[u][t][0]) : gather(b.tl[u][t]);
                         const int src = as_cm ? r + 16 * u : 4 * r + u;
                         sa[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(b.sar[t])));
                     }
@@ -1781,9 +1803,13 @@ FP8BG_TILED(FP8BG_TILED_LAUNCHER)
         if (a.split_last)                                                                     \
             hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kSkinnyLast>), g, dim3(64 * S), shm, \
                                s, a);                                                         \
+        else if (NT == 1 && a.M <= 8)                                                         \
+            hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, (NT == 1 ? kSkinnyFewTokens : 0)>), g, \
+                               dim3(64 * S), shm, s, a);                                      \
         else                                                                                  \
             hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, 0>), g, dim3(64 * S), shm, s, a); \
     }
+// (launches with at most 8 tokens on 16-token tiles take the few-token load)
 FP8BG_SKINNY(FP8BG_SKINNY_LAUNCHER)
 #undef FP8BG_SKINNY_LAUNCHER
 
