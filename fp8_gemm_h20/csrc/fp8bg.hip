@@ -1195,7 +1195,8 @@ void fp8bg_ring_dp(KArgs a) {
 // l >> 3, chunk l & 7): half the L1 accesses of the two loads that cover 16
 // rows, which at M <= 8 cost as much as the weights' own loads.  The same
 // eight ds_bpermute passes give MFMA lane (r, q) chunks q and 4 + q of row
-// r & 7; bitwise the same C as the general path.
+// r & 7; bitwise the same C as the general path.  Taken on tiles of 16 and
+// 32 weight rows (see the skinny launcher).
 constexpr int kSkinnyQuant = 1, kSkinnyLast = 2, kSkinnyQuantFew = 4, kSkinnyFewTokens = 8;
 template <int NWB, int NTB, int S, int U, int MODE>
 __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
@@ -1803,13 +1804,16 @@ FP8BG_TILED(FP8BG_TILED_LAUNCHER)
         if (a.split_last)                                                                     \
             hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kSkinnyLast>), g, dim3(64 * S), shm, \
                                s, a);                                                         \
-        else if (NT == 1 && a.M <= 8)                                                         \
-            hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, (NT == 1 ? kSkinnyFewTokens : 0)>), g, \
-                               dim3(64 * S), shm, s, a);                                      \
+        else if (NT == 1 && NW <= 2 && a.M <= 8)                                              \
+            hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U,                                    \
+                                             (NT == 1 && NW <= 2 ? kSkinnyFewTokens : 0)>),   \
+                               g, dim3(64 * S), shm, s, a);                                   \
         else                                                                                  \
             hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, 0>), g, dim3(64 * S), shm, s, a); \
     }
-// (launches with at most 8 tokens on 16-token tiles take the few-token load)
+// (launches with at most 8 tokens on 16-token tiles of 16 or 32 weight rows
+// take the few-token load; on 64-row tiles it measured 15% slower cold at
+// (12288, 2048) M = 4 and 8, and 1-3% faster on the others)
 FP8BG_SKINNY(FP8BG_SKINNY_LAUNCHER)
 #undef FP8BG_SKINNY_LAUNCHER
 
