@@ -11,7 +11,7 @@ from pathlib import Path
 
 LIB_NAME = "libfp8bg.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 OK = 0
 ERR_SHAPE = 1
@@ -55,6 +55,7 @@ EXPORTS = (
     "fp8bg_quant_act",
     "fp8bg_e4m3_encode_host",
     "fp8bg_calib_mfma",
+    "fp8bg_calib_mfma_promoted",
     "fp8bg_calib_read",
     "fp8bg_calib_write",
     "fp8bg_calib_launch",
@@ -151,6 +152,8 @@ def _declare(lib):
     lib.fp8bg_e4m3_encode_host.restype = ctypes.c_int
     lib.fp8bg_calib_mfma.argtypes = [vp, vp, i32, i32, vp]
     lib.fp8bg_calib_mfma.restype = ctypes.c_int
+    lib.fp8bg_calib_mfma_promoted.argtypes = [vp, vp, vp, i32, i32, vp]
+    lib.fp8bg_calib_mfma_promoted.restype = ctypes.c_int
     lib.fp8bg_calib_read.argtypes = [vp, i64, vp, i32, vp]
     lib.fp8bg_calib_read.restype = ctypes.c_int
     lib.fp8bg_calib_write.argtypes = [vp, i64, ctypes.c_uint32, i32, i32, vp]

@@ -1,6 +1,8 @@
-"""Calibration of the GPU this runs on: the FP8 MFMA rate and the streaming
-read and write rates it sustains, measured with the library's calibration
-kernels (fp8bg_calib_mfma, fp8bg_calib_read, fp8bg_calib_write).  They are reported next to the
+"""Calibration of the GPU this runs on: the FP8 MFMA rate (alone, and with the
+block-scale promotion of every product) and the streaming read and write
+rates it sustains, measured with the library's calibration kernels
+(fp8bg_calib_mfma, fp8bg_calib_mfma_promoted, fp8bg_calib_read,
+fp8bg_calib_write).  They are reported next to the
 published peaks (5.0 PFLOP/s dense FP8, 8 TB/s HBM) that the roofline
 fractions divide by, as the share of those peaks the chip itself reaches.
 """
@@ -31,23 +33,31 @@ def _time(torch, stream, launch, reps):
     return statistics.median(vals)
 
 
-def mfma_rate(torch, device, stream, iters=4096, workgroups_per_cu=2, reps=5):
+def mfma_rate(torch, device, stream, iters=4096, workgroups_per_cu=2, reps=5, promoted=False):
     """Dense FP8 MFMA rate: workgroups_per_cu workgroups of 4 waves on every
-    CU, each wave issuing 16 MFMAs per iteration.  Checks every output
+    CU (two waves per SIMD by default, as the 256x256 GEMM tile runs), each
+    wave issuing 16 MFMAs per iteration; with promoted, each product is
+    promoted by four FMAs as in the GEMM kernels.  Checks every output
     (2048 * iters) and returns TFLOP/s."""
     lib = _lib.lib()
     wgs = _num_cus(device) * workgroups_per_cu
     codes = torch.full((32 * 64,), ONE_CODES, dtype=torch.int32, device=device)
+    scale = torch.ones(64, dtype=torch.float32, device=device)
     out = torch.empty(wgs * 256, dtype=torch.float32, device=device)
+    name = "fp8bg_calib_mfma_promoted" if promoted else "fp8bg_calib_mfma"
 
     def launch():
-        _lib.check(lib.fp8bg_calib_mfma(codes.data_ptr(), out.data_ptr(), wgs, iters,
-                                        stream.cuda_stream))
+        if promoted:
+            _lib.check(lib.fp8bg_calib_mfma_promoted(codes.data_ptr(), scale.data_ptr(), out.data_ptr(),
+                                                     wgs, iters, stream.cuda_stream))
+        else:
+            _lib.check(lib.fp8bg_calib_mfma(codes.data_ptr(), out.data_ptr(), wgs, iters,
+                                            stream.cuda_stream))
     with torch.cuda.stream(stream):
         us = _time(torch, stream, launch, reps)
     torch.cuda.synchronize(device)
     if not bool((out == 2048.0 * iters).all()):
-        raise RuntimeError("fp8bg_calib_mfma: wrong result")
+        raise RuntimeError(f"{name}: wrong result")
     flops = wgs * 4 * iters * MFMA_PER_ITER * MFMA_FLOPS
     return {"tflops": round(flops / us / 1e6, 1), "us": round(us, 1), "workgroups": wgs,
             "iters": iters}

@@ -1962,6 +1962,45 @@ __global__ __launch_bounds__(256) void fp8bg_calib_mfma_kernel(const int32_t* co
     out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc[0][0] + acc[1][0] + acc[2][0] + acc[3][0];
 }
 
+// The same MFMAs as the GEMM kernels take them: each product starts from a
+// zero accumulator and is promoted at once by four FMAs with a scale read
+// at run time (1.0), into 8 accumulators; the FMAs of one product follow
+// the next MFMA, as in the ring kernel's loop.  out = 2048 * iters as
+// above.  Its rate against fp8bg_calib_mfma_kernel's is what the block-scale
+// promotion costs the matrix pipe.  A product from a zero accumulator is a
+// pure function of its operands, so the empty asm before each MFMA gives
+// the compiler a new A operand every time: without it, the 16 MFMAs of an
+// iteration fold into the 4 distinct (A, B) pairs.
+__global__ __launch_bounds__(256) void fp8bg_calib_promote_kernel(const int32_t* codes,
+                                                                  const float* scale, float* out,
+                                                                  int iters) {
+    const int lane = threadIdx.x & 63;
+    i32x8 a[2], b[2];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        a[0][e] = codes[(0 * 8 + e) * 64 + lane];
+        a[1][e] = codes[(1 * 8 + e) * 64 + lane];
+        b[0][e] = codes[(2 * 8 + e) * 64 + lane];
+        b[1][e] = codes[(3 * 8 + e) * 64 + lane];
+    }
+    float sc = scale[lane];
+    f32x4 acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < iters; ++it) {
+        asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]), "+v"(sc));
+#pragma unroll
+        for (int u = 0; u < kCalibMfmaPerIter; ++u) {
+            asm volatile("" : "+v"(a[u & 1]));
+            promote(acc[u & 7], mfma16x16x128(a[u & 1], b[(u >> 1) & 1]), sc);
+        }
+    }
+    float r = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) r += acc[c][0];
+    out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = r;
+}
+
 // Grid-stride read of n16 16-byte words, four loads in flight per lane,
 // XOR-folded; one 32-bit word per thread is written.
 __global__ __launch_bounds__(256) void fp8bg_calib_read_kernel(const i32x4* src, int64_t n16,
@@ -2352,6 +2391,16 @@ int fp8bg_calib_mfma(const int32_t* codes, float* out, int32_t workgroups, int32
     if ((((uintptr_t)codes) & 3) || (((uintptr_t)out) & 3)) return FP8BG_ERR_ALIGN;
     hipLaunchKernelGGL(fp8bg_calib_mfma_kernel, dim3((unsigned)workgroups), dim3(256), 0,
                        (hipStream_t)stream, (const int32_t*)codes, out, iters);
+    return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
+}
+
+int fp8bg_calib_mfma_promoted(const int32_t* codes, const float* scale, float* out, int32_t workgroups,
+                              int32_t iters, void* stream) {
+    if (!codes || !scale || !out) return FP8BG_ERR_NULL;
+    if (workgroups < 1 || iters < 1 || iters > FP8BG_CALIB_MAX_ITERS) return FP8BG_ERR_SHAPE;
+    if ((((uintptr_t)codes) & 3) || (((uintptr_t)scale) & 3) || (((uintptr_t)out) & 3)) return FP8BG_ERR_ALIGN;
+    hipLaunchKernelGGL(fp8bg_calib_promote_kernel, dim3((unsigned)workgroups), dim3(256), 0,
+                       (hipStream_t)stream, (const int32_t*)codes, scale, out, iters);
     return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
 }
 

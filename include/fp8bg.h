@@ -43,7 +43,7 @@ extern "C" {
 
 /* ABI version returned by fp8bg_version(); bumped on any signature or struct
  * change. */
-#define FP8BG_ABI_VERSION 8
+#define FP8BG_ABI_VERSION 9
 
 /* ---- kernel kinds --------------------------------------------------------- */
 /* LDS-tiled kernel: a block_w x block_t workgroup tile, 4 waves in a
@@ -295,6 +295,12 @@ int fp8bg_e4m3_encode_host(const float* x, uint8_t* out, int64_t n);
  * 256 floats.  With every code byte 0x38 (1.0) each out value is
  * 2048 * iters exactly.
  *
+ * fp8bg_calib_mfma_promoted: the same MFMAs as the GEMM kernels issue them,
+ * each product from a zero accumulator and promoted at once by four FMAs
+ * with the scale scale[lane] (64 floats, 1.0 for the exact result) into 8
+ * accumulators; same arguments and result as fp8bg_calib_mfma.  The ratio of
+ * the two rates is what the block-scale promotion costs the matrix pipe.
+ *
  * fp8bg_calib_read: reads `bytes` (a multiple of 16, src 16-byte aligned)
  * with `workgroups` workgroups of 256 threads and writes workgroups * 256
  * uint32 words whose XOR equals the XOR of all 32-bit words of src.
@@ -311,6 +317,8 @@ int fp8bg_e4m3_encode_host(const float* x, uint8_t* out, int64_t n);
 #define FP8BG_CALIB_MAX_ITERS 8192
 int fp8bg_calib_mfma(const int32_t* codes, float* out, int32_t workgroups, int32_t iters,
                      void* stream);
+int fp8bg_calib_mfma_promoted(const int32_t* codes, const float* scale, float* out, int32_t workgroups,
+                              int32_t iters, void* stream);
 int fp8bg_calib_read(const void* src, int64_t bytes, uint32_t* out, int32_t workgroups,
                      void* stream);
 int fp8bg_calib_write(void* dst, int64_t bytes, uint32_t value, int32_t workgroups, int32_t nontemporal,
