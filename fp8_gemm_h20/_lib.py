@@ -11,7 +11,7 @@ from pathlib import Path
 
 LIB_NAME = "libfp8bg.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 OK = 0
 ERR_SHAPE = 1
@@ -42,6 +42,7 @@ FLAG_SCALE_LDS = 0x1
 FLAG_XCD_REMAP = 0x2
 FLAG_SWZ8 = 0x4
 FLAG_SWZPAIR = 0x8
+FLAG_B_SHUFFLED = 0x10
 
 # Every symbol include/fp8bg.h declares.
 EXPORTS = (
@@ -53,6 +54,7 @@ EXPORTS = (
     "fp8bg_gemm_noalloc",
     "fp8bg_gemm_bf16a",
     "fp8bg_quant_act",
+    "fp8bg_shuffle_b",
     "fp8bg_e4m3_encode_host",
     "fp8bg_calib_mfma",
     "fp8bg_calib_mfma_promoted",
@@ -148,6 +150,8 @@ def _declare(lib):
     lib.fp8bg_gemm_bf16a.restype = ctypes.c_int
     lib.fp8bg_quant_act.argtypes = [vp, i64, vp, vp, i64, i64, i32, i32, ctypes.c_float, vp]
     lib.fp8bg_quant_act.restype = ctypes.c_int
+    lib.fp8bg_shuffle_b.argtypes = [vp, i64, vp, i32, i32, vp]
+    lib.fp8bg_shuffle_b.restype = ctypes.c_int
     lib.fp8bg_e4m3_encode_host.argtypes = [vp, vp, i64]
     lib.fp8bg_e4m3_encode_host.restype = ctypes.c_int
     lib.fp8bg_calib_mfma.argtypes = [vp, vp, i32, i32, vp]

@@ -66,6 +66,10 @@ constexpr int kThreads = 256;
 constexpr int kGroupK = 128;          // K elements per scale group
 constexpr int kRowBytes = kGroupK;    // one fp8 row of a group = 128 bytes
 constexpr int kMaxLds = 160 * 1024;   // gfx950 LDS per workgroup
+// Shuffled B (FP8BG_FLAG_B_SHUFFLED): one 16-row block of one 128-K group,
+// stored in MFMA lane order; byte 16 l + 1024 h + e of block (b, g) is
+// B[16 b + (l & 15), 128 g + 64 h + 16 (l >> 4) + e] (l < 64, h < 2, e < 16)
+constexpr int kShufBlock = 16 * kGroupK;
 
 // Scale-area DMA instructions per wave and stage of the ring kernel: one
 // 64-dword slice per wave carries the tile's As column (tt floats), its Bs
@@ -242,6 +246,27 @@ __device__ __forceinline__ int xcd_remap(int pid, int n) {
 __device__ __forceinline__ int swz(int r, int mode) {
     return mode == 1 ? (r & 7) : mode == 2 ? ((r >> 1) & 7) : ((r & 7) ^ ((r >> 3) & 1));
 }
+
+// The ring kernel's swizzle.  Its operand reads give lane l = r + 16 q the
+// logical chunks q and q + 4 (the skinny kernel's K order), and a
+// ds_read_b128 serves together the eight lanes that agree in l % 8: rows
+// k and k + 8 at chunks q = 0 .. 3.  Their eight slots q ^ swz(k) and
+// q ^ swz(k + 8) are distinct when swz(k) ^ swz(k + 8) has bit 2 set; with
+// mode 0 of swz() (bit 0) every such read took a 2-way conflict (7x the
+// SQ_LDS_BANK_CONFLICT cycles, 2.5% slower at M=16384 N=12288 K=2048).
+//   mode 0: swz = (r & 7) ^ 5 ((r >> 3) & 1)   (also keeps any 16
+//           consecutive rows at one chunk on distinct 16-byte bank groups)
+//   modes 1, 2 as swz()
+__device__ __forceinline__ int swz_ring(int r, int mode) {
+    return mode == 1 ? (r & 7) : mode == 2 ? ((r >> 1) & 7) : ((r & 7) ^ (((r >> 3) & 1) * 5));
+}
+
+// Shuffled B in the ring's LDS: MFMA lane l's 16 bytes of a block half sit
+// at slot l ^ ((l >> 3) & 7), so the eight lanes that a ds_read_b128 serves
+// together (equal l % 8) read eight different bank groups; the DMA lane that
+// writes slot i fetches the block's chunk of lane i ^ ((i >> 3) & 7) (the map
+// is its own inverse), still 64 contiguous bytes per quad of lanes.
+__device__ __forceinline__ int shuf_slot(int l) { return l ^ ((l >> 3) & 7); }
 
 // Grouped tile order (GROUP_SIZE_M semantics, reference
 // kernels/baseline_triton.py:36-45): runs of group_t token tiles sweep the
@@ -501,10 +526,10 @@ struct First {
 // of the stacked [weights; tokens] tile (TW + TT rows of 128 bytes) is copied
 // global -> LDS by global_load_lds_dwordx4: one instruction moves 64 lanes x
 // 16 bytes = 8 rows into a contiguous 1 KB block, lane l writing chunk slot
-// l % 8 of row l / 8.  The lane fetches global chunk (l % 8) ^ swz(row), so
-// chunk c of a row sits at slot c ^ swz(row): the XOR swizzle that spreads
-// the MFMA operand reads (16 consecutive lanes = 16 consecutive rows, same
-// chunk) over the LDS banks.  The group's scales travel the same way: one
+// l % 8 of row l / 8.  The lane fetches global chunk (l % 8) ^ swz_ring(row),
+// so chunk c of a row sits at slot c ^ swz_ring(row): the XOR swizzle that
+// spreads the MFMA operand reads (16 consecutive lanes = 16 consecutive rows,
+// four chunks across the wave) over the LDS banks.  The group's scales travel the same way: one
 // global_load_lds_dword per wave fills a 64-float slice of the stage's scale
 // area with the tile's As column (slots 0 .. TT-1) and its Bs values (slots
 // TT .. TT + TW/128 - 1).  ST stages form a ring: the loads of group
@@ -533,8 +558,11 @@ constexpr bool ring_has_dp(int TW, int TT, int KF, int KU, int WK) {
 constexpr bool ring_has_last(int TT, int KF) { return TT <= 64 && KF == 0; }
 
 // The ring kernel's body.  DPO: every workgroup of the launch is a whole
-// (data-parallel) tile, none computes a K split.
-template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK, bool DPO, bool LAST>
+// (data-parallel) tile, none computes a K split.  BSH: B in the shuffled
+// layout (kShufBlock); its 16-row blocks reach LDS in MFMA lane order, so
+// each wave reads a weight operand as two lane-linear 16-byte loads.
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK, bool DPO, bool LAST,
+          bool BSH = false>
 __device__ __forceinline__ void ring_body(const KArgs& a) {
     constexpr int NWAVE = WW * WT;                // waves of one K slice
     constexpr int WTW = TW / WW;
@@ -605,6 +633,8 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         __builtin_amdgcn_make_buffer_rsrc((void*)a.A, (short)0, (int)((uint32_t)a.M * (uint32_t)a.K), kBufferFlags);
     const __amdgpu_buffer_rsrc_t rsB =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.B, (short)0, (int)((uint32_t)a.N * (uint32_t)a.K), kBufferFlags);
+    // (shuffled B: operand block b of the weights is half b % 2 of the
+    // tile's 16-row block b / 2, copied as it lies, 16 bytes per lane)
     bool from_b[NJ];
     uint32_t soff[NJ];
     int dblk[NJ];
@@ -614,9 +644,13 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         const int b = b_raw < NBLK ? b_raw : b_raw - NBLK;
         dblk[j] = b;
         const int row = 8 * b + (lane >> 3);
-        const int chunk = (lane & 7) ^ swz(row, a.swz);
+        const int chunk = (lane & 7) ^ swz_ring(row, a.swz);
         from_b[j] = 8 * b < TW;                   // wave-uniform
-        if (from_b[j])
+        if (from_b[j] && BSH)
+            soff[j] = (uint32_t)min((w0 >> 4) + (b >> 1), (a.N >> 4) - 1) * (uint32_t)(a.K / kGroupK) *
+                          (uint32_t)kShufBlock +
+                      (b & 1) * (kShufBlock / 2) + shuf_slot(lane) * 16;
+        else if (from_b[j])
             soff[j] = (uint32_t)min(w0 + row, a.N - 1) * (uint32_t)a.K + chunk * 16;
         else
             soff[j] = (uint32_t)min(t0 + row - TW, a.M - 1) * (uint32_t)a.K + chunk * 16;
@@ -653,7 +687,9 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
     auto dma_block = [&](int j, int g, int stage) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(from_b[j] ? rsB : rsA,
                                                  FP8BG_LDS_PTR(lds + stage * STAGE + dblk[j] * 1024), 16,
-                                                 soff[j], (uint32_t)g * kGroupK, 0, 0);
+                                                 soff[j],
+                                                 (uint32_t)g * (BSH && from_b[j] ? kShufBlock : kGroupK), 0,
+                                                 0);
     };
     auto dma_scales = [&](int g, int stage) {
 #pragma unroll
@@ -674,16 +710,28 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
     // merged into every path by the compiler).
     f32x4 acc[NW][NT];
 
-    // Operand reads: lane l reads row r0 + (l & 15) of a 16-row block at
-    // chunks c0 and c0 ^ 1.  The lane's two byte offsets inside a stage are
-    // fixed; the block's row r0 (wave-uniform) becomes the read's immediate
-    // offset, so a group adds only the stage base to the two lane offsets.
-    const int c0 = ((lane >> 4) * 2) ^ swz(lane & 15, a.swz);
-    const uint32_t lane_lo = (lane & 15) * kRowBytes + (c0 << 4);
-    const uint32_t lane_hi = (lane & 15) * kRowBytes + ((c0 ^ 1) << 4);
+    // Operand reads: lane l = r + 16 q reads row r0 + r of a 16-row block at
+    // chunks q and q + 4 (K bytes [16 q, +16) and [64 + 16 q, +16): the order
+    // of the skinny kernel and of the shuffled layout, so that every kernel
+    // feeds each MFMA the same bytes from either B layout).  The lane's two
+    // byte offsets inside a stage are fixed; the block's row r0 (wave-
+    // uniform) becomes the read's immediate offset, so a group adds only the
+    // stage base to the two lane offsets.  The weights of a shuffled B sit in
+    // lane order, permuted by shuf_slot: bytes 16 shuf_slot(l) and 1024 + the
+    // same of their block.
+    const int sw_l = swz_ring(lane & 15, a.swz);
+    const uint32_t lane_lo = (lane & 15) * kRowBytes + (((lane >> 4) ^ sw_l) << 4);
+    const uint32_t lane_hi = (lane & 15) * kRowBytes + ((((lane >> 4) + 4) ^ sw_l) << 4);
     auto opread = [&](const unsigned char* st, int r0) -> i32x8 {
         const i32x4 lo = *(const i32x4*)(st + lane_lo + r0 * kRowBytes);
         const i32x4 hi = *(const i32x4*)(st + lane_hi + r0 * kRowBytes);
+        return (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+    const uint32_t wlane_lo = BSH ? 16 * shuf_slot(lane) : lane_lo;
+    const uint32_t wlane_hi = BSH ? kShufBlock / 2 + 16 * shuf_slot(lane) : lane_hi;
+    auto wread = [&](const unsigned char* st, int r0) -> i32x8 {
+        const i32x4 lo = *(const i32x4*)(st + wlane_lo + r0 * kRowBytes);
+        const i32x4 hi = *(const i32x4*)(st + wlane_hi + r0 * kRowBytes);
         return (i32x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
 
@@ -727,7 +775,7 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         i32x8 wop[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-            wop[w] = opread(st, wv_w * WTW + w * 16);
+            wop[w] = wread(st, wv_w * WTW + w * 16);
             __builtin_amdgcn_sched_barrier(0);
         }
         const float sb = sc[TT + (w0 % 128 + wv_w * WTW) / 128];
@@ -818,7 +866,7 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         i32x8 top = opread(st, TW + wv_t * WTT);
         i32x8 wop[NW];
 #pragma unroll
-        for (int w = 0; w < NW; ++w) wop[w] = opread(st, wv_w * WTW + w * 16);
+        for (int w = 0; w < NW; ++w) wop[w] = wread(st, wv_w * WTW + w * 16);
         const float sb = sc[TT + (w0 % 128 + wv_w * WTW) / 128];
         const int r = lane & 15, qd = lane >> 4;
         // byte offsets of the lane's C chunks inside a 16-row block
@@ -1163,6 +1211,26 @@ void fp8bg_ring_dp(KArgs a) {
     ring_body<TW, TT, WW, WT, ST, KF, KU, WK, true, false>(a);
 }
 
+// The three ring kernels for a shuffled B (FP8BG_FLAG_B_SHUFFLED).
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK>
+__global__ __launch_bounds__(64 * WW * WT * WK)
+__attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
+void fp8bg_ring_bs(KArgs a) {
+    ring_body<TW, TT, WW, WT, ST, KF, KU, WK, false, false, true>(a);
+}
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK>
+__global__ __launch_bounds__(64 * WW * WT * WK)
+__attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
+void fp8bg_ring_last_bs(KArgs a) {
+    ring_body<TW, TT, WW, WT, ST, KF, KU, WK, false, true, true>(a);
+}
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK>
+__global__ __launch_bounds__(64 * WW * WT * WK)
+__attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
+void fp8bg_ring_dp_bs(KArgs a) {
+    ring_body<TW, TT, WW, WT, ST, KF, KU, WK, true, false, true>(a);
+}
+
 // ===========================================================================
 // Small-M kernel: operands straight from global memory, waves split K
 // ===========================================================================
@@ -1197,13 +1265,19 @@ void fp8bg_ring_dp(KArgs a) {
 // eight ds_bpermute passes give MFMA lane (r, q) chunks q and 4 + q of row
 // r & 7; bitwise the same C as the general path.  Taken on tiles of 16 and
 // 32 weight rows (see the skinny launcher).
-constexpr int kSkinnyQuant = 1, kSkinnyLast = 2, kSkinnyQuantFew = 4, kSkinnyFewTokens = 8;
+// kSkinnyBShuf: B in the shuffled layout (FP8BG_FLAG_B_SHUFFLED): the 2 KB
+// of a 16-row block's 128-K group are stored in MFMA lane order, so lane l's
+// loads at bytes 16 l and 1024 + 16 l of the block are its operand as they
+// arrive, and the weights need no ds_bpermute.
+constexpr int kSkinnyQuant = 1, kSkinnyLast = 2, kSkinnyQuantFew = 4, kSkinnyFewTokens = 8,
+              kSkinnyBShuf = 16;
 template <int NWB, int NTB, int S, int U, int MODE>
 __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     constexpr int TW = 16 * NWB, TT = 16 * NTB, NB = NWB * NTB;
     constexpr bool QA = MODE & kSkinnyQuant, LAST = MODE & kSkinnyLast;
     constexpr bool QF = MODE & kSkinnyQuantFew;
     constexpr bool FT = MODE & kSkinnyFewTokens;
+    constexpr bool BSH = MODE & kSkinnyBShuf;
     static_assert(!QF || (QA && NTB == 1), "the few-token quantiser takes one 16-token tile");
     static_assert(!FT || (!QA && NTB == 1), "the few-token load takes one 16-token tile of fp8 tokens");
     __shared__ f32x4 red[S][NB][64];
@@ -1251,9 +1325,13 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     const bool as_cm = a.as_sm == 1;
     const int sa_row = as_cm ? (lane & 15) : lr, sa_u = as_cm ? (lane >> 4) : lc;
     const float* bsp = a.Bs + (int64_t)(w0 >> 7) * a.bs_sn;
+    // shuffled B: block (b, g) of 16 rows and one group at (b K/128 + g) 2 KB
+    const int KGB = a.K / kGroupK;
     const uint8_t* wp[NWB];
 #pragma unroll
-    for (int w = 0; w < NWB; ++w) wp[w] = a.B + (size_t)min(w0 + 16 * w + lr, a.N - 1) * a.K + 16 * lc;
+    for (int w = 0; w < NWB; ++w)
+        wp[w] = BSH ? a.B + (size_t)min((w0 >> 4) + w, (a.N >> 4) - 1) * KGB * kShufBlock + 16 * lane
+                    : a.B + (size_t)min(w0 + 16 * w + lr, a.N - 1) * a.K + 16 * lc;
     const uint8_t* tp[NTB];
     const float* asp[NTB];
     const uint16_t* xp[NTB];
@@ -1306,10 +1384,11 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const size_t go = (size_t)group(j0 + u) * kGroupK;
+            const size_t gw = BSH ? (size_t)group(j0 + u) * kShufBlock : go;
 #pragma unroll
             for (int w = 0; w < NWB; ++w) {
-                b.wl[u][w][0] = *(const i32x4*)(wp[w] + go);
-                b.wl[u][w][1] = *(const i32x4*)(wp[w] + go + 64);
+                b.wl[u][w][0] = *(const i32x4*)(wp[w] + gw);
+                b.wl[u][w][1] = *(const i32x4*)(wp[w] + gw + (BSH ? kShufBlock / 2 : 64));
             }
 #pragma unroll
             for (int t = 0; t < NTB; ++t) {
@@ -1486,7 +1565,10 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                 }
 #pragma unroll
                 for (int w = 0; w < NWB; ++w) {
-                    const i32x8 wv = gather(b.wl[u][w]);
+                    const i32x8 wv = BSH ? (i32x8){b.wl[u][w][0][0], b.wl[u][w][0][1], b.wl[u][w][0][2],
+                                                   b.wl[u][w][0][3], b.wl[u][w][1][0], b.wl[u][w][1][1],
+                                                   b.wl[u][w][1][2], b.wl[u][w][1][3]}
+                                         : gather(b.wl[u][w]);
 #pragma unroll
                     for (int t = 0; t < NTB; ++t) promote(acc[w][t], mfma16x16x128(wv, tv[t]), sa[t] * sb);
                 }
@@ -1662,6 +1744,22 @@ __host__ __device__ inline uint32_t e4m3_from_f32(float f) {
     return sign | ((((r >> 23) - 120u) << 3) | ((r >> 20) & 7u));
 }
 
+// Row-major e4m3 B [N, K] (row stride ldb bytes) -> the shuffled layout
+// (kShufBlock): thread c of the grid-stride loop writes the 16 bytes at
+// 16 c, so the stores are contiguous; each reads 16 bytes of one row.
+__global__ __launch_bounds__(kThreads) void fp8bg_shuffle_b_kernel(const uint8_t* b, int64_t ldb,
+                                                                   uint8_t* bt, int64_t chunks, int kg) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += stride) {
+        const int64_t blk = c >> 7;                      // 128 chunks per block
+        const int in = (int)(c & 127), h = in >> 6, l = in & 63;
+        const int64_t nb = blk / kg, g = blk - nb * kg;
+        const int64_t row = 16 * nb + (l & 15);
+        const int64_t col = 128 * g + 64 * h + 16 * (l >> 4);
+        *(i32x4*)(bt + 16 * c) = *(const i32x4*)(b + row * ldb + col);
+    }
+}
+
 struct QArgs {
     const uint16_t* x;     // bf16 [M, K], row stride ldx elements
     uint8_t* q;            // e4m3 [M, K], row stride K
@@ -1785,99 +1883,95 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(1, 1, 16, 1) X(1, 1, 16, 2) X(2, 1, 16, 1) X(2, 1, 16, 2)                \
     X(1, 2, 16, 1) X(2, 2, 16, 1)
 
+typedef void (*LaunchFn)(dim3 grid, size_t shm, hipStream_t s, const KArgs& a);
 struct Instance {
     int kind, tw, tt, ww, wt, wk, unroll, stages, kf, threads;
-    void (*launch)(dim3 grid, size_t shm, hipStream_t s, const KArgs& a);
+    LaunchFn launch;       // row-major B
+    LaunchFn launch_bs;    // shuffled B (FP8BG_FLAG_B_SHUFFLED); null: not supported
 };
 
-#define FP8BG_TILED_LAUNCHER(TW, TT, WW, WT, KF)                                             \
-    static void tiled_##TW##_##TT##_##WW##_##WT##_##KF(dim3 g, size_t shm, hipStream_t s,   \
-                                                       const KArgs& a) {                    \
-        hipLaunchKernelGGL((fp8bg_tiled<TW, TT, WW, WT, KF>), g, dim3(kThreads), shm, s, a); \
-    }
-FP8BG_TILED(FP8BG_TILED_LAUNCHER)
-#undef FP8BG_TILED_LAUNCHER
+template <int TW, int TT, int WW, int WT, int KF>
+void tiled_launch(dim3 g, size_t shm, hipStream_t s, const KArgs& a) {
+    hipLaunchKernelGGL((fp8bg_tiled<TW, TT, WW, WT, KF>), g, dim3(kThreads), shm, s, a);
+}
 
-#define FP8BG_SKINNY_LAUNCHER(NW, NT, S, U)                                                  \
-    static void skinny_##NW##_##NT##_##S##_##U(dim3 g, size_t shm, hipStream_t s,           \
-                                               const KArgs& a) {                            \
-        if (a.split_last)                                                                     \
-            hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kSkinnyLast>), g, dim3(64 * S), shm, \
-                               s, a);                                                         \
-        else if (NT == 1 && NW <= 2 && a.M <= 8)                                              \
-            hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U,                                    \
-                                             (NT == 1 && NW <= 2 ? kSkinnyFewTokens : 0)>),   \
-                               g, dim3(64 * S), shm, s, a);                                   \
-        else                                                                                  \
-            hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, 0>), g, dim3(64 * S), shm, s, a); \
-    }
+// BM: the B-layout MODE bit (0 or kSkinnyBShuf).
 // (launches with at most 8 tokens on 16-token tiles of 16 or 32 weight rows
 // take the few-token load; on 64-row tiles it measured 15% slower cold at
 // (12288, 2048) M = 4 and 8, and 1-3% faster on the others)
-FP8BG_SKINNY(FP8BG_SKINNY_LAUNCHER)
-#undef FP8BG_SKINNY_LAUNCHER
+template <int NW, int NT, int S, int U, int BM>
+void skinny_launch(dim3 g, size_t shm, hipStream_t s, const KArgs& a) {
+    constexpr int kFewTok = NT == 1 && NW <= 2 ? kSkinnyFewTokens : 0;
+    if (a.split_last)
+        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kSkinnyLast>), g, dim3(64 * S), shm, s, a);
+    else if (kFewTok && a.M <= 8)
+        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kFewTok>), g, dim3(64 * S), shm, s, a);
+    else
+        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM>), g, dim3(64 * S), shm, s, a);
+}
 
 // (launches with at most 4 tokens on 16-token tiles take the few-token
 // quantiser: same codes and scales, a fraction of the per-value work)
-#define FP8BG_SKINNY_QA_LAUNCHER(NW, NT, S, U)                                               \
-    static void skinny_qa_##NW##_##NT##_##S##_##U(dim3 g, size_t shm, hipStream_t s,        \
-                                                  const KArgs& a) {                         \
-        constexpr int kFew = kSkinnyQuant | kSkinnyQuantFew;                                  \
-        if constexpr (NT == 1) {                                                              \
-            if (a.M <= 4) {                                                                   \
-                if (a.split_last)                                                             \
-                    hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kFew | kSkinnyLast>), g,   \
-                                       dim3(64 * S), shm, s, a);                              \
-                else                                                                          \
-                    hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kFew>), g, dim3(64 * S),   \
-                                       shm, s, a);                                            \
-                return;                                                                       \
-            }                                                                                 \
-        }                                                                                     \
-        if (a.split_last)                                                                     \
-            hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kSkinnyQuant | kSkinnyLast>), g,   \
-                               dim3(64 * S), shm, s, a);                                      \
-        else                                                                                  \
-            hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kSkinnyQuant>), g, dim3(64 * S),   \
-                               shm, s, a);                                                    \
+template <int NW, int NT, int S, int U, int BM>
+void skinny_qa_launch(dim3 g, size_t shm, hipStream_t s, const KArgs& a) {
+    constexpr int kQ = BM | kSkinnyQuant;
+    if constexpr (NT == 1) {
+        if (a.M <= 4) {
+            if (a.split_last)
+                hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kQ | kSkinnyQuantFew | kSkinnyLast>), g,
+                                   dim3(64 * S), shm, s, a);
+            else
+                hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kQ | kSkinnyQuantFew>), g, dim3(64 * S),
+                                   shm, s, a);
+            return;
+        }
     }
-FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_LAUNCHER)
-#undef FP8BG_SKINNY_QA_LAUNCHER
+    if (a.split_last)
+        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kQ | kSkinnyLast>), g, dim3(64 * S), shm, s, a);
+    else
+        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, kQ>), g, dim3(64 * S), shm, s, a);
+}
 
-#define FP8BG_RING_LAUNCHER(TW, TT, WW, WT, ST, KF, KU, WK)                                  \
-    static void ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF##_##KU##_##WK(                   \
-        dim3 g, size_t shm, hipStream_t s, const KArgs& a) {                                  \
-        if constexpr (ring_has_last(TT, KF)) {                                                 \
-            if (a.split_last) {                                                               \
-                hipLaunchKernelGGL((fp8bg_ring_last<TW, TT, WW, WT, ST, KF, KU, WK>), g,     \
-                                   dim3(64 * WW * WT * WK), shm, s, a);                       \
-                return;                                                                       \
-            }                                                                                 \
-        }                                                                                     \
-        if constexpr (ring_has_dp(TW, TT, KF, KU, WK)) {                                      \
-            if (a.n_dp == (int)g.x && a.kcount > KU) {                                        \
-                hipLaunchKernelGGL((fp8bg_ring_dp<TW, TT, WW, WT, ST, KF, KU, WK>), g,       \
-                                   dim3(64 * WW * WT * WK), shm, s, a);                       \
-                return;                                                                       \
-            }                                                                                 \
-        }                                                                                     \
-        hipLaunchKernelGGL((fp8bg_ring<TW, TT, WW, WT, ST, KF, KU, WK>), g,                  \
-                           dim3(64 * WW * WT * WK), shm, s, a);                               \
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK, bool BSH>
+void ring_launch(dim3 g, size_t shm, hipStream_t s, const KArgs& a) {
+    const dim3 block(64 * WW * WT * WK);
+    if constexpr (ring_has_last(TT, KF)) {
+        if (a.split_last) {
+            if constexpr (BSH)
+                hipLaunchKernelGGL((fp8bg_ring_last_bs<TW, TT, WW, WT, ST, KF, KU, WK>), g, block, shm, s, a);
+            else
+                hipLaunchKernelGGL((fp8bg_ring_last<TW, TT, WW, WT, ST, KF, KU, WK>), g, block, shm, s, a);
+            return;
+        }
     }
-FP8BG_RING(FP8BG_RING_LAUNCHER)
-#undef FP8BG_RING_LAUNCHER
+    if constexpr (ring_has_dp(TW, TT, KF, KU, WK)) {
+        if (a.n_dp == (int)g.x && a.kcount > KU) {
+            if constexpr (BSH)
+                hipLaunchKernelGGL((fp8bg_ring_dp_bs<TW, TT, WW, WT, ST, KF, KU, WK>), g, block, shm, s, a);
+            else
+                hipLaunchKernelGGL((fp8bg_ring_dp<TW, TT, WW, WT, ST, KF, KU, WK>), g, block, shm, s, a);
+            return;
+        }
+    }
+    if constexpr (BSH)
+        hipLaunchKernelGGL((fp8bg_ring_bs<TW, TT, WW, WT, ST, KF, KU, WK>), g, block, shm, s, a);
+    else
+        hipLaunchKernelGGL((fp8bg_ring<TW, TT, WW, WT, ST, KF, KU, WK>), g, block, shm, s, a);
+}
 
 #define FP8BG_TILED_ENTRY(TW, TT, WW, WT, KF) \
-    {FP8BG_KIND_TILED, TW, TT, WW, WT, 1, 1, 1, KF, kThreads, tiled_##TW##_##TT##_##WW##_##WT##_##KF},
-#define FP8BG_SKINNY_ENTRY(NW, NT, S, U) \
-    {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 1, 0, 64 * S, skinny_##NW##_##NT##_##S##_##U},
-#define FP8BG_RING_ENTRY(TW, TT, WW, WT, ST, KF, KU, WK)                          \
-    {FP8BG_KIND_RING, TW, TT, WW, WT, WK, KU, ST, KF, 64 * WW * WT * WK,          \
-     ring_##TW##_##TT##_##WW##_##WT##_##ST##_##KF##_##KU##_##WK},
+    {FP8BG_KIND_TILED, TW, TT, WW, WT, 1, 1, 1, KF, kThreads, tiled_launch<TW, TT, WW, WT, KF>, nullptr},
+#define FP8BG_SKINNY_ENTRY(NW, NT, S, U)                                                  \
+    {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 1, 0, 64 * S,                       \
+     skinny_launch<NW, NT, S, U, 0>, skinny_launch<NW, NT, S, U, kSkinnyBShuf>},
+#define FP8BG_RING_ENTRY(TW, TT, WW, WT, ST, KF, KU, WK)                                  \
+    {FP8BG_KIND_RING, TW, TT, WW, WT, WK, KU, ST, KF, 64 * WW * WT * WK,                  \
+     ring_launch<TW, TT, WW, WT, ST, KF, KU, WK, false>, ring_launch<TW, TT, WW, WT, ST, KF, KU, WK, true>},
 const Instance kInstances[] = {FP8BG_TILED(FP8BG_TILED_ENTRY) FP8BG_SKINNY(FP8BG_SKINNY_ENTRY)
                                    FP8BG_RING(FP8BG_RING_ENTRY)};
-#define FP8BG_SKINNY_QA_ENTRY(NW, NT, S, U) \
-    {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 1, 0, 64 * S, skinny_qa_##NW##_##NT##_##S##_##U},
+#define FP8BG_SKINNY_QA_ENTRY(NW, NT, S, U)                                               \
+    {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 1, 0, 64 * S,                       \
+     skinny_qa_launch<NW, NT, S, U, 0>, skinny_qa_launch<NW, NT, S, U, kSkinnyBShuf>},
 const Instance kQaInstances[] = {FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_ENTRY)};
 #undef FP8BG_TILED_ENTRY
 #undef FP8BG_SKINNY_ENTRY
@@ -2088,12 +2182,13 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     if (cfg->split < 1 || cfg->group_t < 1 || num_cus < 1) return FP8BG_ERR_CONFIG;
     if (cfg->split_mode < FP8BG_SPLIT_NONE || cfg->split_mode > FP8BG_SPLIT_LAST) return FP8BG_ERR_CONFIG;
     if (cfg->flags & ~(FP8BG_FLAG_SCALE_LDS | FP8BG_FLAG_XCD_REMAP | FP8BG_FLAG_SWZ8 |
-                       FP8BG_FLAG_SWZPAIR))
+                       FP8BG_FLAG_SWZPAIR | FP8BG_FLAG_B_SHUFFLED))
         return FP8BG_ERR_CONFIG;
     if ((cfg->flags & FP8BG_FLAG_SWZ8) && (cfg->flags & FP8BG_FLAG_SWZPAIR)) return FP8BG_ERR_CONFIG;
     const int kg = K / 128;
     const Instance& k = kInstances[ki];
     if (k.kf && kg != k.kf) return FP8BG_ERR_CONFIG;
+    if ((cfg->flags & FP8BG_FLAG_B_SHUFFLED) && !k.launch_bs) return FP8BG_ERR_CONFIG;
     const bool skinny = k.kind == FP8BG_KIND_SKINNY;
     const bool ring = k.kind == FP8BG_KIND_RING;
     if ((skinny || ring) && (cfg->flags & FP8BG_FLAG_SCALE_LDS)) return FP8BG_ERR_CONFIG;
@@ -2215,7 +2310,7 @@ int gemm_enqueue(const void* A, const void* B, const float* As, int64_t as_strid
     a.swz = (cfg->flags & FP8BG_FLAG_SWZ8) ? 1 : (cfg->flags & FP8BG_FLAG_SWZPAIR) ? 2 : 0;
     const size_t shm = a.scale_lds ? (size_t)k.tt * (K / 128) * sizeof(float) : 0;
     hipStream_t s = (hipStream_t)stream;
-    k.launch(dim3(p.grid), shm, s, a);
+    ((cfg->flags & FP8BG_FLAG_B_SHUFFLED) ? k.launch_bs : k.launch)(dim3(p.grid), shm, s, a);
     if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
     if (p.n_split > 0 && !a.split_last) {
         const int parts = reduce_parts(p, k, num_cus);
@@ -2347,7 +2442,7 @@ int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps, const void* B
     a.qs_sm = s_stride_m;
     a.qs_sk = s_stride_k;
     hipStream_t s = (hipStream_t)stream;
-    k.launch(dim3(p.grid), 0, s, a);
+    ((cfg->flags & FP8BG_FLAG_B_SHUFFLED) ? k.launch_bs : k.launch)(dim3(p.grid), 0, s, a);
     if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
     if (p.n_split > 0 && !a.split_last) {
         const int parts = reduce_parts(p, k, num_cus);
@@ -2381,6 +2476,23 @@ int fp8bg_quant_act(const void* x, int64_t x_stride_m, void* q, float* s, int64_
     a.eps = eps;
     hipLaunchKernelGGL(fp8bg_quant_act_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
                        (hipStream_t)stream, a);
+    return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
+}
+
+int fp8bg_shuffle_b(const void* B, int64_t b_stride_n, void* Bt, int32_t N, int32_t K, void* stream) {
+    if (!B || !Bt) return FP8BG_ERR_NULL;
+    if (N < 16 || N % 16 || K < 128 || K % 128 || b_stride_n < K) return FP8BG_ERR_SHAPE;
+    if ((((uintptr_t)B) | ((uintptr_t)Bt) | (uintptr_t)b_stride_n) & 15) return FP8BG_ERR_ALIGN;
+    const uint8_t* b = (const uint8_t*)B;
+    const uint8_t* bt = (const uint8_t*)Bt;
+    // the output must not overlap the rows it reads (no in-place shuffle)
+    const uint8_t* b_end = b + (int64_t)(N - 1) * b_stride_n + K;
+    if (bt < b_end && b < bt + (int64_t)N * K) return FP8BG_ERR_SHAPE;
+    const int64_t chunks = (int64_t)N * K / 16;
+    const int64_t want = (chunks + kThreads - 1) / kThreads;
+    const int64_t blocks = want < 4096 ? want : 4096;
+    hipLaunchKernelGGL(fp8bg_shuffle_b_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
+                       (hipStream_t)stream, b, b_stride_n, (uint8_t*)Bt, chunks, K / 128);
     return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
 }
 

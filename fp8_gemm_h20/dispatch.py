@@ -2,6 +2,17 @@
 from .config import _has_fused_table, _select, _select_fused
 from .engine import run
 
+_SHUF_BLOCK = 2048      # bytes of one 16-row x 128-K block of a shuffled weight
+
+
+def _shuffled(B):
+    return B.ndim == 3 and B.shape[2] == _SHUF_BLOCK
+
+
+def _weight_dims(B):
+    """(N, K) of a row-major [N, K] weight or of a shuffled one."""
+    return (B.shape[0] * 16, B.shape[1] * 128) if _shuffled(B) else tuple(B.shape)
+
 
 def matmul(A, B, As, Bs, *, profile="35b_tp1", bias=None, out=None):
     """FP8 A[M,K], B[N,K] with fp32 block scales -> bf16 C[M,N] on A's device.
@@ -15,13 +26,15 @@ def matmul(A, B, As, Bs, *, profile="35b_tp1", bias=None, out=None):
     `bias` - bf16 [N] added in the kernel epilogue, bit-identical to a
     separate bf16 `C + bias` (the adapter's sgl_patch/fp8mm_sglang_patch.py:55-56);
     `out` - a contiguous bf16 [M, N] tensor on A's device to write into
-    instead of allocating C (returned).
+    instead of allocating C (returned);
+    B may also be the [N/16, K/128, 2048] tensor that shuffle_weight returns
+    (same C, bit for bit; faster weight loads at small M).
     """
     import torch
-    if A.ndim != 2 or B.ndim != 2:
+    if A.ndim != 2 or (B.ndim != 2 and not _shuffled(B)):
         raise ValueError("A and B must be rank-2 tensors")
     m, k = A.shape
-    n, bk = B.shape
+    n, bk = _weight_dims(B)
     if k != bk or k % 128 or n % 128:
         raise ValueError("A/B dimensions must match and N,K must be multiples of 128")
     if A.dtype != torch.float8_e4m3fn or B.dtype != torch.float8_e4m3fn:
@@ -45,6 +58,28 @@ def matmul(A, B, As, Bs, *, profile="35b_tp1", bias=None, out=None):
         if bias is None and out is None:
             return run(entry, (A, B, As, Bs))
         return run(entry, (A, B, As, Bs), bias=bias, out=out)
+
+
+def shuffle_weight(B):
+    """e4m3 B[N, K] -> the same weight in the shuffled layout, a new
+    [N/16, K/128, 2048] tensor that matmul and linear take in place of B.
+
+    Each 2048-byte block holds 16 rows x 128 K of B in the order the MFMA
+    operands are loaded (C ABI fp8bg_shuffle_b), so the kernels read the
+    weights coalesced and use them without exchanging bytes between lanes.
+    The result of every GEMM is bitwise the one with B.  A one-time
+    transform for weights that stay resident (one HIP kernel, no host sync);
+    no counterpart in the reference, whose adapter keeps B row-major.
+    """
+    import torch
+    from . import kernels
+    if B.ndim != 2 or B.dtype != torch.float8_e4m3fn or not B.is_cuda or not B.is_contiguous():
+        raise ValueError("B must be a contiguous rank-2 float8_e4m3fn CUDA tensor")
+    n, k = B.shape
+    if n % 128 or k % 128:
+        raise ValueError("A/B dimensions must match and N,K must be multiples of 128")
+    with torch.cuda.device(B.device):
+        return kernels.shuffle_b(B)
 
 
 def quantize_act(x, *, eps=1e-10, column_major_scales=False):
@@ -93,11 +128,12 @@ def linear(x, B, Bs, *, profile="35b_tp1", bias=None, eps=1e-10, fused=None):
     kernels ("use").  Without one, the fused launch runs where the matmul
     entry itself is a skinny configuration with a fused instance.
     fused=False forces the two-kernel path, fused=True the fused one
-    (ValueError where no fused configuration applies).
+    (ValueError where no fused configuration applies).  B may be a shuffled
+    weight (shuffle_weight).
     """
     import torch
     from . import kernels
-    n, k = B.shape
+    n, k = _weight_dims(B)
     if fused is not False and x.dtype == torch.bfloat16 and x.is_cuda and x.shape[-1] == k \
             and x.numel() > 0:
         m = x.numel() // k
@@ -137,7 +173,9 @@ def _fused_choice(profile, m, n, k):
 def _check_weights(B, Bs, device, bias):
     """Weight-side checks of matmul (dispatch.py:12-27 order) for the fused linear."""
     import torch
-    n, k = B.shape
+    if B.ndim != 2 and not _shuffled(B):
+        raise ValueError("A and B must be rank-2 tensors")
+    n, k = _weight_dims(B)
     if k % 128 or n % 128:
         raise ValueError("A/B dimensions must match and N,K must be multiples of 128")
     if B.dtype != torch.float8_e4m3fn:

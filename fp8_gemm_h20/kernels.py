@@ -261,11 +261,52 @@ def _workspace(dev, ws_elems):
     return bufs.get(ws_elems)
 
 
+# shuffled B (C ABI fp8bg_shuffle_b): N/16 x K/128 blocks of 2048 bytes, held
+# as a [N/16, K/128, 2048] e4m3 tensor so that its layout shows in its shape
+SHUF_BLOCK = 2048
+
+
+def is_shuffled(B):
+    """True for a weight in the shuffled layout ([N/16, K/128, 2048])."""
+    return B.dim() == 3 and B.shape[2] == SHUF_BLOCK
+
+
+def weight_dims(B):
+    """(N, K) of a row-major [N, K] or a shuffled weight."""
+    if is_shuffled(B):
+        return B.shape[0] * 16, B.shape[1] * 128
+    return tuple(B.shape)
+
+
+def shuffle_b(B):
+    """Row-major e4m3 B [N, K] (unit column stride, 16-byte row stride) ->
+    the shuffled layout, as a new [N/16, K/128, 2048] tensor on B's device."""
+    import torch
+    n, k = B.shape
+    bt = torch.empty((n // 16, k // 128, SHUF_BLOCK), device=B.device, dtype=B.dtype)
+    stream = torch.cuda.current_stream(B.device).cuda_stream
+    _lib.check(_lib.lib().fp8bg_shuffle_b(B.data_ptr(), B.stride(0), bt.data_ptr(), n, k, stream))
+    return bt
+
+
+def _layout_struct(cstruct, B):
+    """The config struct for B's layout: a copy with FLAG_B_SHUFFLED for a
+    shuffled B (tiled configurations do not read it: ValueError)."""
+    if not is_shuffled(B):
+        return cstruct
+    if cstruct.kind == _lib.KIND_TILED:
+        raise ValueError("a shuffled B needs a skinny or ring configuration")
+    c = _lib.Config.from_buffer_copy(cstruct)
+    c.flags |= _lib.FLAG_B_SHUFFLED
+    return c
+
+
 def check_operands(M, N, K, B, As, Bs, bias=None, out=None):
     """The kernels take M, N, K and raw pointers; operands whose shapes
     disagree with them would be read or written out of bounds, so they are
     refused here (ValueError) before anything is launched."""
-    if (tuple(B.shape) != (N, K) or (As is not None and tuple(As.shape) != (M, K // 128))
+    b_shape = (N // 16, K // 128, SHUF_BLOCK) if is_shuffled(B) else (N, K)
+    if (tuple(B.shape) != b_shape or N % 16 or (As is not None and tuple(As.shape) != (M, K // 128))
             or tuple(Bs.shape) != (N // 128, K // 128)
             or (bias is not None and tuple(bias.shape) != (N,))
             or (out is not None and tuple(out.shape) != (M, N))):
@@ -279,8 +320,9 @@ def launch(A, B, As, Bs, cstruct, bias=None, out=None):
     when None); `bias` is an optional bf16 [N] added in the epilogue."""
     import torch
     M, K = A.shape
-    N = B.shape[0]
+    N = weight_dims(B)[0]
     check_operands(M, N, K, B, As, Bs, bias, out)
+    cstruct = _layout_struct(cstruct, B)
     dev = A.device
     cus = num_cus(dev)
     plan = _lib.make_plan(M, N, K, cstruct, cus)
@@ -324,10 +366,10 @@ def linear_fused(x2, B, Bs, config, eps, bias=None, out=None, keep_quantized=Fal
     keep_quantized is set."""
     import torch
     m, k = x2.shape
-    n = B.shape[0]
+    n = weight_dims(B)[0]
     check_operands(m, n, k, B, None, Bs, bias, out)
     dev = x2.device
-    cstruct = _skinny_cached(_freeze(config))
+    cstruct = _layout_struct(_skinny_cached(_freeze(config)), B)
     cus = num_cus(dev)
     plan = _lib.make_plan(m, n, k, cstruct, cus)
     C = torch.empty((m, n), device=dev, dtype=torch.bfloat16) if out is None else out
@@ -402,7 +444,7 @@ def ring(A, B, As, Bs, config, **epilogue):
     if m1 and A.shape[0] > m1 and "TAIL" in config:
         import torch
         from .engine import run
-        m, n = A.shape[0], B.shape[0]
+        m, n = A.shape[0], weight_dims(B)[0]
         out = epilogue.get("out")
         C = torch.empty((m, n), device=A.device, dtype=torch.bfloat16) if out is None else out
         head = {k: v for k, v in config.items() if k not in ("M_SPLIT", "TAIL")}

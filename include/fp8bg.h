@@ -9,6 +9,7 @@
  * OCP e4m3 ("float8_e4m3fn") row-major with row stride K, As[M,K/128] and
  * Bs[N/128,K/128] are fp32 with arbitrary element strides, and C is row-major
  * bf16 with row stride N (round-to-nearest-even from the fp32 accumulator).
+ * B may instead be given in the shuffled layout (FP8BG_FLAG_B_SHUFFLED).
  *
  * The reference (qiuuuuu622/fp8_gemm_h20) has no C ABI: its kernels are
  * Python-level Triton/Gluon host wrappers with the signature
@@ -43,7 +44,7 @@ extern "C" {
 
 /* ABI version returned by fp8bg_version(); bumped on any signature or struct
  * change. */
-#define FP8BG_ABI_VERSION 9
+#define FP8BG_ABI_VERSION 10
 
 /* ---- kernel kinds --------------------------------------------------------- */
 /* LDS-tiled kernel: a block_w x block_t workgroup tile, 4 waves in a
@@ -103,10 +104,16 @@ extern "C" {
 /* Remap workgroup ids so that consecutive tiles run on the same XCD (L2). */
 #define FP8BG_FLAG_XCD_REMAP 0x2
 /* LDS chunk swizzle of the tiled and ring kernels (chunk c of row r is stored
- * at slot c ^ swz(r)); default swz = (r & 7) ^ ((r >> 3) & 1), free of bank
- * conflicts for the MFMA operand reads.  At most one of: */
+ * at slot c ^ swz(r)); default swz = (r & 7) ^ ((r >> 3) & 1) (tiled) and
+ * (r & 7) ^ 5 ((r >> 3) & 1) (ring), free of bank conflicts for each
+ * kernel's MFMA operand reads.  At most one of: */
 #define FP8BG_FLAG_SWZ8      0x4   /* swz = r & 7 */
 #define FP8BG_FLAG_SWZPAIR   0x8   /* swz = (r >> 1) & 7 */
+/* B is in the shuffled layout that fp8bg_shuffle_b writes (skinny and ring
+ * kernels; a tiled configuration with it is FP8BG_ERR_CONFIG).  Every kernel
+ * gives each MFMA the same operand bytes from either layout, so C is bitwise
+ * the same as with the row-major B it was made from. */
+#define FP8BG_FLAG_B_SHUFFLED 0x10
 
 /*
  * Kernel configuration: one gfx950 table entry (fp8_gemm_h20/configs/<profile>.json).
@@ -274,6 +281,22 @@ int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps,
                      int32_t num_cus, float* ws, int64_t ws_elems,
                      void* q_out, float* s_out, int64_t s_stride_m,
                      int64_t s_stride_k, void* stream);
+
+/*
+ * Weight layout for MFMA-friendly loads (no reference counterpart: the
+ * reference's adapter keeps B row-major; its survey ranks a pre-shuffled
+ * weight format as an optional later step).  Writes the row-major e4m3
+ * B[N,K] (row stride b_stride_n bytes, a multiple of 16) into Bt (N*K
+ * bytes) as N/16 x K/128 blocks of 2048 bytes, block (b, g) at byte
+ * (b * K/128 + g) * 2048, and inside it
+ *     Bt[block + 16 l + 1024 h + e] = B[16 b + (l % 16), 128 g + 64 h + 16 (l / 16) + e]
+ * for l < 64, h < 2, e < 16: the bytes that lane l of a wave feeds one
+ * 16x16x128 MFMA, in lane order, so the kernels load them coalesced and use
+ * them without a cross-lane exchange.  Pass Bt with FP8BG_FLAG_B_SHUFFLED in
+ * the configuration (Bs unchanged).  N a multiple of 16, K of 128; B, Bt
+ * 16-byte aligned; Bt must not overlap B.  Stream-ordered, no sync.
+ */
+int fp8bg_shuffle_b(const void* B, int64_t b_stride_n, void* Bt, int32_t N, int32_t K, void* stream);
 
 /*
  * Host copy of the kernels' fp32 -> e4m3 conversion (round to nearest even,
