@@ -13,6 +13,9 @@ Environment (the reference's names, so existing launch scripts keep working):
   FP8MM_ENABLE=1          install the patch when this module is imported
   FP8MM_PROFILE=35b_tp1   or 122b_tp4: the measured shape/config profile
   FP8MM_HOME=/path        prepended to sys.path (where this package lives)
+  FP8MM_SHUFFLE_WEIGHTS=1 also keep each weight in the shuffled layout
+                          (`shuffle_weight`; faster small-M loads, bitwise
+                          the same results, one more copy of the weights)
 
 Loading it into every SGLang process: put a `sitecustomize.py` containing
 `import fp8_gemm_h20.sglang_patch` on PYTHONPATH (the reference's
@@ -57,9 +60,29 @@ def eligible(profile, input, weight, block_size, weight_scale, input_scale, bias
             and supports(profile, input.numel() // k, n, k))
 
 
-def make_linear(orig_linear, profile):
+def shuffled_copy(weight):
+    """The weight in the shuffled layout, made on its first eligible call
+    and kept on the tensor (made again after an in-place change of the
+    weight, which bumps its version counter); the row-major weight stays for
+    SGLang's own paths.  None while a CUDA graph is being captured: a copy
+    made there would live in the graph's memory pool, so a weight first seen
+    during capture runs row-major until an eager call makes its copy."""
+    import torch
+    from . import shuffle_weight
+    held = getattr(weight, "_fp8mm_shuffled", None)
+    if held is not None and held[0] == weight._version:
+        return held[1]
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    held = (weight._version, shuffle_weight(weight))
+    weight._fp8mm_shuffled = held
+    return held[1]
+
+
+def make_linear(orig_linear, profile, shuffle_weights=False):
     """Wrap one of SGLang's block-FP8 linears; `.fp8mm_stats` counts the
-    calls taken here ("ours") and passed through ("fallback")."""
+    calls taken here ("ours") and passed through ("fallback").  With
+    shuffle_weights the GEMM reads each weight's shuffled copy."""
     stats = {"ours": 0, "fallback": 0}
 
     def fp8mm_w8a8_block_fp8_linear(input, weight, block_size, weight_scale, input_scale=None,
@@ -69,7 +92,8 @@ def make_linear(orig_linear, profile):
             return orig_linear(input, weight, block_size, weight_scale, input_scale, bias)
         from . import linear
         stats["ours"] += 1
-        return linear(input, weight, weight_scale, profile=profile,
+        w = shuffled_copy(weight) if shuffle_weights else None
+        return linear(input, weight if w is None else w, weight_scale, profile=profile,
                       bias=None if bias is None else bias.contiguous())
 
     fp8mm_w8a8_block_fp8_linear.fp8mm_stats = stats
@@ -77,11 +101,14 @@ def make_linear(orig_linear, profile):
     return fp8mm_w8a8_block_fp8_linear
 
 
-def patch_module(mod, profile=None):
-    """Install the wrapper into an imported fp8_utils module (idempotent)."""
+def patch_module(mod, profile=None, shuffle_weights=None):
+    """Install the wrapper into an imported fp8_utils module (idempotent).
+    shuffle_weights None: from FP8MM_SHUFFLE_WEIGHTS."""
     if getattr(mod.dispatch_w8a8_block_fp8_linear, "fp8mm_patched", False):
         return
     profile = profile or os.environ.get("FP8MM_PROFILE", "35b_tp1")
+    if shuffle_weights is None:
+        shuffle_weights = os.environ.get("FP8MM_SHUFFLE_WEIGHTS") == "1"
     from .config import get_profile
     get_profile(profile)                       # unknown profile: fail at install, not mid-serve
     orig_dispatch = mod.dispatch_w8a8_block_fp8_linear
@@ -92,36 +119,39 @@ def patch_module(mod, profile=None):
         if not any(orig is getattr(mod, name, None) for name in ROCM_LINEARS):
             return orig
         if orig not in wrapped:
-            wrapped[orig] = make_linear(orig, profile)
+            wrapped[orig] = make_linear(orig, profile, shuffle_weights)
         return wrapped[orig]
 
     patched_dispatch.fp8mm_patched = True
     patched_dispatch.fp8mm_profile = profile
+    patched_dispatch.fp8mm_shuffle_weights = shuffle_weights
     mod.dispatch_w8a8_block_fp8_linear = patched_dispatch
-    print(f"[fp8mm] patched {TARGET}.dispatch_w8a8_block_fp8_linear (profile={profile})",
-          file=sys.stderr, flush=True)
+    print(f"[fp8mm] patched {TARGET}.dispatch_w8a8_block_fp8_linear (profile={profile}"
+          f"{', shuffled weights' if shuffle_weights else ''})", file=sys.stderr, flush=True)
 
 
 class _PatchingLoader(importlib.abc.Loader):
     """Runs the real loader, then patches the freshly executed module."""
 
-    def __init__(self, inner, profile):
+    def __init__(self, inner, profile, shuffle_weights):
         self.inner = inner
         self.profile = profile
+        self.shuffle_weights = shuffle_weights
 
     def create_module(self, spec):
         return self.inner.create_module(spec)
 
     def exec_module(self, module):
         self.inner.exec_module(module)
-        patch_module(module, self.profile)
+        patch_module(module, self.profile, self.shuffle_weights)
 
 
 class PatchFinder(importlib.abc.MetaPathFinder):
     """Meta-path hook that intercepts the import of TARGET."""
 
-    def __init__(self, profile=None):
+    def __init__(self, profile=None, shuffle_weights=None):
         self.profile = profile
+        self.shuffle_weights = shuffle_weights
 
     def find_spec(self, name, path, target=None):
         if name != TARGET:
@@ -129,17 +159,17 @@ class PatchFinder(importlib.abc.MetaPathFinder):
         spec = importlib.machinery.PathFinder.find_spec(name, path)
         if spec is None or spec.loader is None:
             return None
-        spec.loader = _PatchingLoader(spec.loader, self.profile)
+        spec.loader = _PatchingLoader(spec.loader, self.profile, self.shuffle_weights)
         return spec
 
 
-def install(profile=None):
+def install(profile=None, shuffle_weights=None):
     """Patch TARGET now if it is already imported, else when it is imported.
     Returns the meta-path finder (None when the module was patched in place)."""
     if TARGET in sys.modules:
-        patch_module(sys.modules[TARGET], profile)
+        patch_module(sys.modules[TARGET], profile, shuffle_weights)
         return None
-    finder = PatchFinder(profile)
+    finder = PatchFinder(profile, shuffle_weights)
     sys.meta_path.insert(0, finder)
     return finder
 
