@@ -55,6 +55,16 @@
 
 #include "fp8bg.h"
 
+// Build partition: fp8_gemm_h20/build.py compiles this file once per part,
+// in parallel, and links the objects into one library.  Part 1 holds the C
+// ABI, the tiled kernel and the small kernels; parts 2-7 the ring and skinny
+// launchers (and so their kernel instances), split by list half and B
+// layout.  FP8BG_PART 0 (the default) is all of it in one translation unit.
+#ifndef FP8BG_PART
+#define FP8BG_PART 0
+#endif
+#define FP8BG_HOST_PART (FP8BG_PART <= 1)
+
 namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -1689,6 +1699,7 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     }
 }
 
+#if FP8BG_HOST_PART
 // ===========================================================================
 // Split-K reduction: one workgroup per split tile, fixed split order.
 // ===========================================================================
@@ -1808,6 +1819,8 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     if (sub == 0) a.s[m * a.s_sm + g * a.s_sk] = scale;
 }
 
+#endif  // FP8BG_HOST_PART
+
 // ---------------------------------------------------------------------------
 // Compiled instances
 // ---------------------------------------------------------------------------
@@ -1839,32 +1852,35 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
 
 // ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 //        K slices)
-#define FP8BG_RING(X)                                           \
+#define FP8BG_RING_A(X) \
     X(256, 128, 4, 1, 3, 0, 1, 1) X(256, 128, 2, 2, 3, 0, 1, 1) \
     X(128, 128, 2, 2, 4, 0, 1, 1) X(128, 128, 4, 1, 4, 0, 1, 1) \
-    X(128, 128, 2, 2, 3, 0, 1, 1) X(128, 64, 2, 2, 4, 0, 1, 1)  \
-    X(128, 64, 4, 1, 4, 0, 1, 1) X(128, 64, 2, 2, 3, 0, 1, 1)   \
-    X(64, 64, 4, 1, 4, 0, 1, 1) X(256, 64, 4, 1, 3, 0, 1, 1)    \
-    X(128, 32, 4, 1, 4, 0, 1, 1) X(256, 256, 4, 2, 2, 0, 1, 1)  \
+    X(128, 128, 2, 2, 3, 0, 1, 1) X(128, 64, 2, 2, 4, 0, 1, 1) \
+    X(128, 64, 4, 1, 4, 0, 1, 1) X(128, 64, 2, 2, 3, 0, 1, 1) \
+    X(64, 64, 4, 1, 4, 0, 1, 1) X(256, 64, 4, 1, 3, 0, 1, 1) \
+    X(128, 32, 4, 1, 4, 0, 1, 1) X(256, 256, 4, 2, 2, 0, 1, 1) \
     X(256, 128, 4, 2, 3, 0, 1, 1) X(256, 128, 4, 2, 2, 0, 1, 1) \
     X(128, 256, 2, 4, 2, 0, 1, 1) X(256, 128, 4, 1, 2, 2, 1, 1) \
-    X(128, 128, 2, 2, 2, 2, 1, 1) X(64, 64, 4, 1, 8, 0, 1, 1)   \
-    X(128, 64, 4, 1, 6, 0, 1, 1) X(128, 32, 4, 1, 7, 0, 1, 1)   \
+    X(128, 128, 2, 2, 2, 2, 1, 1) X(64, 64, 4, 1, 8, 0, 1, 1) \
+    X(128, 64, 4, 1, 6, 0, 1, 1) X(128, 32, 4, 1, 7, 0, 1, 1) \
     X(128, 128, 2, 2, 2, 0, 1, 1) X(192, 256, 3, 4, 2, 0, 1, 1) \
     X(192, 128, 6, 2, 2, 0, 1, 1) X(192, 128, 6, 2, 3, 0, 1, 1) \
-    X(192, 128, 3, 4, 3, 0, 1, 1) X(192, 64, 6, 2, 4, 0, 1, 1)  \
-    X(64, 64, 4, 1, 4, 0, 2, 1) X(64, 64, 4, 1, 8, 0, 2, 1)     \
-    X(64, 64, 4, 1, 8, 0, 4, 1) X(128, 64, 4, 1, 4, 0, 2, 1)    \
-    X(128, 64, 4, 1, 6, 0, 2, 1) X(128, 32, 4, 1, 4, 0, 2, 1)   \
-    X(128, 32, 4, 1, 7, 0, 2, 1) X(128, 64, 2, 2, 4, 0, 2, 1)   \
-    X(192, 64, 6, 2, 4, 0, 2, 1) X(64, 64, 4, 1, 4, 0, 2, 2)    \
-    X(64, 64, 4, 1, 8, 0, 2, 2) X(64, 64, 4, 1, 8, 0, 4, 2)     \
-    X(64, 64, 4, 1, 8, 0, 4, 4) X(128, 64, 4, 1, 6, 0, 2, 2)    \
-    X(128, 32, 4, 1, 4, 0, 2, 2) X(128, 128, 4, 2, 2, 0, 1, 1)   \
-    X(128, 128, 4, 2, 3, 0, 1, 1) X(128, 128, 4, 2, 4, 0, 2, 1) \
-    X(256, 160, 4, 2, 2, 0, 1, 1) X(256, 192, 4, 2, 2, 0, 1, 1)   \
-    X(128, 160, 2, 2, 3, 0, 1, 1) X(128, 96, 2, 2, 4, 0, 1, 1)    \
-    X(64, 64, 2, 2, 8, 0, 4, 1)
+    X(192, 128, 3, 4, 3, 0, 1, 1)
+
+#define FP8BG_RING_B(X) \
+    X(192, 64, 6, 2, 4, 0, 1, 1) X(64, 64, 4, 1, 4, 0, 2, 1) \
+    X(64, 64, 4, 1, 8, 0, 2, 1) X(64, 64, 4, 1, 8, 0, 4, 1) \
+    X(128, 64, 4, 1, 4, 0, 2, 1) X(128, 64, 4, 1, 6, 0, 2, 1) \
+    X(128, 32, 4, 1, 4, 0, 2, 1) X(128, 32, 4, 1, 7, 0, 2, 1) \
+    X(128, 64, 2, 2, 4, 0, 2, 1) X(192, 64, 6, 2, 4, 0, 2, 1) \
+    X(64, 64, 4, 1, 4, 0, 2, 2) X(64, 64, 4, 1, 8, 0, 2, 2) \
+    X(64, 64, 4, 1, 8, 0, 4, 2) X(64, 64, 4, 1, 8, 0, 4, 4) \
+    X(128, 64, 4, 1, 6, 0, 2, 2) X(128, 32, 4, 1, 4, 0, 2, 2) \
+    X(128, 128, 4, 2, 2, 0, 1, 1) X(128, 128, 4, 2, 3, 0, 1, 1) \
+    X(128, 128, 4, 2, 4, 0, 2, 1) X(256, 160, 4, 2, 2, 0, 1, 1) \
+    X(256, 192, 4, 2, 2, 0, 1, 1) X(128, 160, 2, 2, 3, 0, 1, 1) \
+    X(128, 96, 2, 2, 4, 0, 1, 1) X(64, 64, 2, 2, 8, 0, 4, 1)
+#define FP8BG_RING(X) FP8BG_RING_A(X) FP8BG_RING_B(X)
 
 // skinny with the fused activation quantiser: the 16-, 32- and 64-token
 // tiles ((4, 1, 8, 4), (4, 1, 4, 4), (4, 1, 16, 1), (2, 4, 8, 2), (1, 4, 16, 1)
@@ -1883,7 +1899,11 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(1, 1, 16, 1) X(1, 1, 16, 2) X(2, 1, 16, 1) X(2, 1, 16, 2)                \
     X(1, 2, 16, 1) X(2, 2, 16, 1)
 
-typedef void (*LaunchFn)(dim3 grid, size_t shm, hipStream_t s, const KArgs& a);
+// Launchers, one per compiled instance and B layout; the skinny and ring
+// ones pick the kernel variant at run time.  The arguments travel by pointer
+// so that a launcher compiled in another part of the build (external
+// functions of plain types, below) can fill the table of part 1.
+typedef void (*LaunchFn)(dim3 grid, size_t shm, hipStream_t s, const void* a);
 struct Instance {
     int kind, tw, tt, ww, wt, wk, unroll, stages, kf, threads;
     LaunchFn launch;       // row-major B
@@ -1891,8 +1911,8 @@ struct Instance {
 };
 
 template <int TW, int TT, int WW, int WT, int KF>
-void tiled_launch(dim3 g, size_t shm, hipStream_t s, const KArgs& a) {
-    hipLaunchKernelGGL((fp8bg_tiled<TW, TT, WW, WT, KF>), g, dim3(kThreads), shm, s, a);
+void tiled_launch(dim3 g, size_t shm, hipStream_t s, const void* a) {
+    hipLaunchKernelGGL((fp8bg_tiled<TW, TT, WW, WT, KF>), g, dim3(kThreads), shm, s, *(const KArgs*)a);
 }
 
 // BM: the B-layout MODE bit (0 or kSkinnyBShuf).
@@ -1900,7 +1920,8 @@ void tiled_launch(dim3 g, size_t shm, hipStream_t s, const KArgs& a) {
 // take the few-token load; on 64-row tiles it measured 15% slower cold at
 // (12288, 2048) M = 4 and 8, and 1-3% faster on the others)
 template <int NW, int NT, int S, int U, int BM>
-void skinny_launch(dim3 g, size_t shm, hipStream_t s, const KArgs& a) {
+void skinny_launch(dim3 g, size_t shm, hipStream_t s, const void* av) {
+    const KArgs& a = *(const KArgs*)av;
     constexpr int kFewTok = NT == 1 && NW <= 2 ? kSkinnyFewTokens : 0;
     if (a.split_last)
         hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kSkinnyLast>), g, dim3(64 * S), shm, s, a);
@@ -1913,7 +1934,8 @@ void skinny_launch(dim3 g, size_t shm, hipStream_t s, const KArgs& a) {
 // (launches with at most 4 tokens on 16-token tiles take the few-token
 // quantiser: same codes and scales, a fraction of the per-value work)
 template <int NW, int NT, int S, int U, int BM>
-void skinny_qa_launch(dim3 g, size_t shm, hipStream_t s, const KArgs& a) {
+void skinny_qa_launch(dim3 g, size_t shm, hipStream_t s, const void* av) {
+    const KArgs& a = *(const KArgs*)av;
     constexpr int kQ = BM | kSkinnyQuant;
     if constexpr (NT == 1) {
         if (a.M <= 4) {
@@ -1933,7 +1955,8 @@ void skinny_qa_launch(dim3 g, size_t shm, hipStream_t s, const KArgs& a) {
 }
 
 template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK, bool BSH>
-void ring_launch(dim3 g, size_t shm, hipStream_t s, const KArgs& a) {
+void ring_launch(dim3 g, size_t shm, hipStream_t s, const void* av) {
+    const KArgs& a = *(const KArgs*)av;
     const dim3 block(64 * WW * WT * WK);
     if constexpr (ring_has_last(TT, KF)) {
         if (a.split_last) {
@@ -1959,19 +1982,103 @@ void ring_launch(dim3 g, size_t shm, hipStream_t s, const KArgs& a) {
         hipLaunchKernelGGL((fp8bg_ring<TW, TT, WW, WT, ST, KF, KU, WK>), g, block, shm, s, a);
 }
 
+}  // namespace
+
+// The launchers' external names (L: rm = row-major B, bs = shuffled B), and
+// for each part either their definitions (the part that compiles them, or
+// all in part 0) or their declarations (part 1, whose table takes them).
+#define FP8BG_RING_FN(TW, TT, WW, WT, ST, KF, KU, WK, L) \
+    fp8bg_ring_##L##_##TW##_##TT##_##WW##_##WT##_##ST##_##KF##_##KU##_##WK
+#define FP8BG_SKINNY_FN(NW, NT, S, U, L) fp8bg_skinny_##L##_##NW##_##NT##_##S##_##U
+#define FP8BG_SKINNY_QA_FN(NW, NT, S, U, L) fp8bg_skinny_qa_##L##_##NW##_##NT##_##S##_##U
+#define FP8BG_LAUNCH_ARGS dim3 g, size_t shm, hipStream_t s, const void* a
+// (linked across the parts, not exported from the library)
+#define FP8BG_LAUNCHER __attribute__((visibility("hidden"))) void
+
+#define FP8BG_RING_DEF_RM(TW, TT, WW, WT, ST, KF, KU, WK)                            \
+    FP8BG_LAUNCHER FP8BG_RING_FN(TW, TT, WW, WT, ST, KF, KU, WK, rm)(FP8BG_LAUNCH_ARGS) {      \
+        ring_launch<TW, TT, WW, WT, ST, KF, KU, WK, false>(g, shm, s, a);            \
+    }
+#define FP8BG_RING_DEF_BS(TW, TT, WW, WT, ST, KF, KU, WK)                            \
+    FP8BG_LAUNCHER FP8BG_RING_FN(TW, TT, WW, WT, ST, KF, KU, WK, bs)(FP8BG_LAUNCH_ARGS) {      \
+        ring_launch<TW, TT, WW, WT, ST, KF, KU, WK, true>(g, shm, s, a);             \
+    }
+#define FP8BG_RING_DECL_RM(TW, TT, WW, WT, ST, KF, KU, WK) \
+    FP8BG_LAUNCHER FP8BG_RING_FN(TW, TT, WW, WT, ST, KF, KU, WK, rm)(FP8BG_LAUNCH_ARGS);
+#define FP8BG_RING_DECL_BS(TW, TT, WW, WT, ST, KF, KU, WK) \
+    FP8BG_LAUNCHER FP8BG_RING_FN(TW, TT, WW, WT, ST, KF, KU, WK, bs)(FP8BG_LAUNCH_ARGS);
+#define FP8BG_SKINNY_DEF_RM(NW, NT, S, U) \
+    FP8BG_LAUNCHER FP8BG_SKINNY_FN(NW, NT, S, U, rm)(FP8BG_LAUNCH_ARGS) { skinny_launch<NW, NT, S, U, 0>(g, shm, s, a); }
+#define FP8BG_SKINNY_DEF_BS(NW, NT, S, U)                                              \
+    FP8BG_LAUNCHER FP8BG_SKINNY_FN(NW, NT, S, U, bs)(FP8BG_LAUNCH_ARGS) {                        \
+        skinny_launch<NW, NT, S, U, kSkinnyBShuf>(g, shm, s, a);                       \
+    }
+#define FP8BG_SKINNY_DECL_RM(NW, NT, S, U) FP8BG_LAUNCHER FP8BG_SKINNY_FN(NW, NT, S, U, rm)(FP8BG_LAUNCH_ARGS);
+#define FP8BG_SKINNY_DECL_BS(NW, NT, S, U) FP8BG_LAUNCHER FP8BG_SKINNY_FN(NW, NT, S, U, bs)(FP8BG_LAUNCH_ARGS);
+#define FP8BG_SKINNY_QA_DEF_RM(NW, NT, S, U)                                           \
+    FP8BG_LAUNCHER FP8BG_SKINNY_QA_FN(NW, NT, S, U, rm)(FP8BG_LAUNCH_ARGS) {                     \
+        skinny_qa_launch<NW, NT, S, U, 0>(g, shm, s, a);                               \
+    }
+#define FP8BG_SKINNY_QA_DEF_BS(NW, NT, S, U)                                           \
+    FP8BG_LAUNCHER FP8BG_SKINNY_QA_FN(NW, NT, S, U, bs)(FP8BG_LAUNCH_ARGS) {                     \
+        skinny_qa_launch<NW, NT, S, U, kSkinnyBShuf>(g, shm, s, a);                    \
+    }
+#define FP8BG_SKINNY_QA_DECL_RM(NW, NT, S, U) FP8BG_LAUNCHER FP8BG_SKINNY_QA_FN(NW, NT, S, U, rm)(FP8BG_LAUNCH_ARGS);
+#define FP8BG_SKINNY_QA_DECL_BS(NW, NT, S, U) FP8BG_LAUNCHER FP8BG_SKINNY_QA_FN(NW, NT, S, U, bs)(FP8BG_LAUNCH_ARGS);
+
+#if FP8BG_PART == 0 || FP8BG_PART == 2
+FP8BG_RING_A(FP8BG_RING_DEF_RM)
+#elif FP8BG_PART == 1
+FP8BG_RING_A(FP8BG_RING_DECL_RM)
+#endif
+#if FP8BG_PART == 0 || FP8BG_PART == 3
+FP8BG_RING_A(FP8BG_RING_DEF_BS)
+#elif FP8BG_PART == 1
+FP8BG_RING_A(FP8BG_RING_DECL_BS)
+#endif
+#if FP8BG_PART == 0 || FP8BG_PART == 4
+FP8BG_RING_B(FP8BG_RING_DEF_RM)
+#elif FP8BG_PART == 1
+FP8BG_RING_B(FP8BG_RING_DECL_RM)
+#endif
+#if FP8BG_PART == 0 || FP8BG_PART == 5
+FP8BG_RING_B(FP8BG_RING_DEF_BS)
+#elif FP8BG_PART == 1
+FP8BG_RING_B(FP8BG_RING_DECL_BS)
+#endif
+#if FP8BG_PART == 0 || FP8BG_PART == 6
+FP8BG_SKINNY(FP8BG_SKINNY_DEF_RM)
+FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_DEF_RM)
+#elif FP8BG_PART == 1
+FP8BG_SKINNY(FP8BG_SKINNY_DECL_RM)
+FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_DECL_RM)
+#endif
+#if FP8BG_PART == 0 || FP8BG_PART == 7
+FP8BG_SKINNY(FP8BG_SKINNY_DEF_BS)
+FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_DEF_BS)
+#elif FP8BG_PART == 1
+FP8BG_SKINNY(FP8BG_SKINNY_DECL_BS)
+FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_DECL_BS)
+#endif
+
+// Everything below is part 1 (and part 0): the instance tables, the host
+// planning code, the small kernels and the C ABI.
+#if FP8BG_HOST_PART
+namespace {
+
 #define FP8BG_TILED_ENTRY(TW, TT, WW, WT, KF) \
     {FP8BG_KIND_TILED, TW, TT, WW, WT, 1, 1, 1, KF, kThreads, tiled_launch<TW, TT, WW, WT, KF>, nullptr},
-#define FP8BG_SKINNY_ENTRY(NW, NT, S, U)                                                  \
-    {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 1, 0, 64 * S,                       \
-     skinny_launch<NW, NT, S, U, 0>, skinny_launch<NW, NT, S, U, kSkinnyBShuf>},
-#define FP8BG_RING_ENTRY(TW, TT, WW, WT, ST, KF, KU, WK)                                  \
-    {FP8BG_KIND_RING, TW, TT, WW, WT, WK, KU, ST, KF, 64 * WW * WT * WK,                  \
-     ring_launch<TW, TT, WW, WT, ST, KF, KU, WK, false>, ring_launch<TW, TT, WW, WT, ST, KF, KU, WK, true>},
+#define FP8BG_SKINNY_ENTRY(NW, NT, S, U)                            \
+    {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 1, 0, 64 * S, \
+     FP8BG_SKINNY_FN(NW, NT, S, U, rm), FP8BG_SKINNY_FN(NW, NT, S, U, bs)},
+#define FP8BG_RING_ENTRY(TW, TT, WW, WT, ST, KF, KU, WK)                        \
+    {FP8BG_KIND_RING, TW, TT, WW, WT, WK, KU, ST, KF, 64 * WW * WT * WK,        \
+     FP8BG_RING_FN(TW, TT, WW, WT, ST, KF, KU, WK, rm), FP8BG_RING_FN(TW, TT, WW, WT, ST, KF, KU, WK, bs)},
 const Instance kInstances[] = {FP8BG_TILED(FP8BG_TILED_ENTRY) FP8BG_SKINNY(FP8BG_SKINNY_ENTRY)
                                    FP8BG_RING(FP8BG_RING_ENTRY)};
-#define FP8BG_SKINNY_QA_ENTRY(NW, NT, S, U)                                               \
-    {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 1, 0, 64 * S,                       \
-     skinny_qa_launch<NW, NT, S, U, 0>, skinny_qa_launch<NW, NT, S, U, kSkinnyBShuf>},
+#define FP8BG_SKINNY_QA_ENTRY(NW, NT, S, U)                         \
+    {FP8BG_KIND_SKINNY, 16 * NW, 16 * NT, 1, 1, S, U, 1, 0, 64 * S, \
+     FP8BG_SKINNY_QA_FN(NW, NT, S, U, rm), FP8BG_SKINNY_QA_FN(NW, NT, S, U, bs)},
 const Instance kQaInstances[] = {FP8BG_SKINNY_QA(FP8BG_SKINNY_QA_ENTRY)};
 #undef FP8BG_TILED_ENTRY
 #undef FP8BG_SKINNY_ENTRY
@@ -2023,6 +2130,8 @@ int find_instance(const fp8bg_config* c) {
 // streaming-read and streaming-write rates this chip sustains, next to the
 // published peaks.
 // ===========================================================================
+namespace {
+
 constexpr int kCalibMfmaPerIter = 16;
 
 // Each wave issues kCalibMfmaPerIter FP8 16x16x128 MFMAs per iteration from
@@ -2139,6 +2248,8 @@ __global__ __launch_bounds__(256) void fp8bg_calib_write_kernel(i32x4* dst, int6
     }
     for (; i < n16; i += stride) put(i);
 }
+
+}  // namespace
 
 extern "C" {
 
@@ -2310,7 +2421,7 @@ int gemm_enqueue(const void* A, const void* B, const float* As, int64_t as_strid
     a.swz = (cfg->flags & FP8BG_FLAG_SWZ8) ? 1 : (cfg->flags & FP8BG_FLAG_SWZPAIR) ? 2 : 0;
     const size_t shm = a.scale_lds ? (size_t)k.tt * (K / 128) * sizeof(float) : 0;
     hipStream_t s = (hipStream_t)stream;
-    ((cfg->flags & FP8BG_FLAG_B_SHUFFLED) ? k.launch_bs : k.launch)(dim3(p.grid), shm, s, a);
+    ((cfg->flags & FP8BG_FLAG_B_SHUFFLED) ? k.launch_bs : k.launch)(dim3(p.grid), shm, s, &a);
     if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
     if (p.n_split > 0 && !a.split_last) {
         const int parts = reduce_parts(p, k, num_cus);
@@ -2442,7 +2553,7 @@ int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps, const void* B
     a.qs_sm = s_stride_m;
     a.qs_sk = s_stride_k;
     hipStream_t s = (hipStream_t)stream;
-    ((cfg->flags & FP8BG_FLAG_B_SHUFFLED) ? k.launch_bs : k.launch)(dim3(p.grid), 0, s, a);
+    ((cfg->flags & FP8BG_FLAG_B_SHUFFLED) ? k.launch_bs : k.launch)(dim3(p.grid), 0, s, &a);
     if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
     if (p.n_split > 0 && !a.split_last) {
         const int parts = reduce_parts(p, k, num_cus);
@@ -2553,3 +2664,5 @@ int fp8bg_e4m3_encode_host(const float* x, uint8_t* out, int64_t n) {
 }
 
 }  // extern "C"
+
+#endif  // FP8BG_HOST_PART
