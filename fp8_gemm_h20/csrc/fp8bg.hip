@@ -1279,8 +1279,13 @@ void fp8bg_ring_dp_bs(KArgs a) {
 // of a 16-row block's 128-K group are stored in MFMA lane order, so lane l's
 // loads at bytes 16 l and 1024 + 16 l of the block are its operand as they
 // arrive, and the weights need no ds_bpermute.
+// kSkinnyOneToken: fp8 tokens for launches with one token.  Only row 0 of the
+// 16-token operand reaches a stored output, so every lane (r, q) loads row
+// 0's chunks q and 4 + q itself, already in the MFMA layout, and the token
+// scale of a group is one value for the wave (v_readlane): no ds_bpermute
+// for the tokens either.  Bitwise the same C as the general path.
 constexpr int kSkinnyQuant = 1, kSkinnyLast = 2, kSkinnyQuantFew = 4, kSkinnyFewTokens = 8,
-              kSkinnyBShuf = 16;
+              kSkinnyBShuf = 16, kSkinnyOneToken = 32;
 template <int NWB, int NTB, int S, int U, int MODE>
 __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     constexpr int TW = 16 * NWB, TT = 16 * NTB, NB = NWB * NTB;
@@ -1288,6 +1293,8 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     constexpr bool QF = MODE & kSkinnyQuantFew;
     constexpr bool FT = MODE & kSkinnyFewTokens;
     constexpr bool BSH = MODE & kSkinnyBShuf;
+    constexpr bool OT = MODE & kSkinnyOneToken;
+    static_assert(!OT || (!QA && !FT && NTB == 1), "the one-token load takes one 16-token tile of fp8 tokens");
     static_assert(!QF || (QA && NTB == 1), "the few-token quantiser takes one 16-token tile");
     static_assert(!FT || (!QA && NTB == 1), "the few-token load takes one 16-token tile of fp8 tokens");
     __shared__ f32x4 red[S][NB][64];
@@ -1355,8 +1362,10 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
             // [64 + 16 (l & 3), +16) (a quad holds the token's whole group)
             xp[t] = a.X + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.ldx + 16 * lc;
         } else {
-            tp[t] = FT ? a.A + (size_t)min(t0 + (lane >> 3), a.M - 1) * a.K + 16 * (lane & 7)
-                       : a.A + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.K + 16 * lc;
+            // (one token: the launch's only token tile starts at row 0)
+            tp[t] = OT   ? a.A + 16 * q
+                    : FT ? a.A + (size_t)min(t0 + (lane >> 3), a.M - 1) * a.K + 16 * (lane & 7)
+                         : a.A + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.K + 16 * lc;
             asp[t] = a.As + (int64_t)min(t0 + 16 * t + sa_row, a.M - 1) * a.as_sm;
         }
     }
@@ -1568,9 +1577,19 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                         tv[t] = gather({(i32x4){o[0], o[1], o[2], o[3]}, (i32x4){o[4], o[5], o[6], o[7]}});
                         sa[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(op_src, __float_as_int(b.sa[u][t])));
                     } else {
-                        tv[t] = FT ? gather_few(b.tl[u][t][0]) : gather(b.tl[u][t]);
                         const int src = as_cm ? r + 16 * u : 4 * r + u;
-                        sa[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(b.sar[t])));
+                        if constexpr (OT) {
+                            // slot u of row 0 sits in lane 16 u (column-major As) or u
+                            tv[t] = (i32x8){b.tl[u][t][0][0], b.tl[u][t][0][1], b.tl[u][t][0][2],
+                                            b.tl[u][t][0][3], b.tl[u][t][1][0], b.tl[u][t][1][1],
+                                            b.tl[u][t][1][2], b.tl[u][t][1][3]};
+                            sa[t] = __int_as_float(
+                                __builtin_amdgcn_readlane(__float_as_int(b.sar[t]), as_cm ? 16 * u : u));
+                        } else {
+                            tv[t] = FT ? gather_few(b.tl[u][t][0]) : gather(b.tl[u][t]);
+                            sa[t] = __int_as_float(
+                                __builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(b.sar[t])));
+                        }
                     }
                 }
 #pragma unroll
@@ -1923,8 +1942,11 @@ template <int NW, int NT, int S, int U, int BM>
 void skinny_launch(dim3 g, size_t shm, hipStream_t s, const void* av) {
     const KArgs& a = *(const KArgs*)av;
     constexpr int kFewTok = NT == 1 && NW <= 2 ? kSkinnyFewTokens : 0;
+    constexpr int kOneTok = NT == 1 ? kSkinnyOneToken : 0;
     if (a.split_last)
         hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kSkinnyLast>), g, dim3(64 * S), shm, s, a);
+    else if (kOneTok && a.M == 1)
+        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kOneTok>), g, dim3(64 * S), shm, s, a);
     else if (kFewTok && a.M <= 8)
         hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kFewTok>), g, dim3(64 * S), shm, s, a);
     else
