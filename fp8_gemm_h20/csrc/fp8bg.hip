@@ -1279,11 +1279,13 @@ void fp8bg_ring_dp_bs(KArgs a) {
 // of a 16-row block's 128-K group are stored in MFMA lane order, so lane l's
 // loads at bytes 16 l and 1024 + 16 l of the block are its operand as they
 // arrive, and the weights need no ds_bpermute.
-// kSkinnyOneToken: fp8 tokens for launches with one token.  Only row 0 of the
-// 16-token operand reaches a stored output, so every lane (r, q) loads row
-// 0's chunks q and 4 + q itself, already in the MFMA layout, and the token
-// scale of a group is one value for the wave (v_readlane): no ds_bpermute
-// for the tokens either.  Bitwise the same C as the general path.
+// kSkinnyOneToken: fp8 tokens loaded in the MFMA layout, for launches with at
+// most two tokens and row-major B (see the skinny launcher).  Rows of the 16-token operand at or past M
+// reach no stored output, so lane (r, q) loads row min(r, M - 1)'s chunks q
+// and 4 + q itself and the tokens need no ds_bpermute; with one token its
+// scale of a group is one value for the wave (v_readlane), else the lane's
+// row's scale comes by ds_bpermute as in the general path.  Bitwise the same
+// C as the general path.
 constexpr int kSkinnyQuant = 1, kSkinnyLast = 2, kSkinnyQuantFew = 4, kSkinnyFewTokens = 8,
               kSkinnyBShuf = 16, kSkinnyOneToken = 32;
 template <int NWB, int NTB, int S, int U, int MODE>
@@ -1362,8 +1364,8 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
             // [64 + 16 (l & 3), +16) (a quad holds the token's whole group)
             xp[t] = a.X + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.ldx + 16 * lc;
         } else {
-            // (one token: the launch's only token tile starts at row 0)
-            tp[t] = OT   ? a.A + 16 * q
+            // (the launch's only token tile starts at row 0)
+            tp[t] = OT   ? a.A + (size_t)min(r, a.M - 1) * a.K + 16 * q
                     : FT ? a.A + (size_t)min(t0 + (lane >> 3), a.M - 1) * a.K + 16 * (lane & 7)
                          : a.A + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.K + 16 * lc;
             asp[t] = a.As + (int64_t)min(t0 + 16 * t + sa_row, a.M - 1) * a.as_sm;
@@ -1579,12 +1581,15 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                     } else {
                         const int src = as_cm ? r + 16 * u : 4 * r + u;
                         if constexpr (OT) {
-                            // slot u of row 0 sits in lane 16 u (column-major As) or u
+                            // one token: slot u of row 0 sits in lane 16 u
+                            // (column-major As) or u
                             tv[t] = (i32x8){b.tl[u][t][0][0], b.tl[u][t][0][1], b.tl[u][t][0][2],
                                             b.tl[u][t][0][3], b.tl[u][t][1][0], b.tl[u][t][1][1],
                                             b.tl[u][t][1][2], b.tl[u][t][1][3]};
-                            sa[t] = __int_as_float(
-                                __builtin_amdgcn_readlane(__float_as_int(b.sar[t]), as_cm ? 16 * u : u));
+                            sa[t] = a.M == 1 ? __int_as_float(__builtin_amdgcn_readlane(
+                                                   __float_as_int(b.sar[t]), as_cm ? 16 * u : u))
+                                             : __int_as_float(__builtin_amdgcn_ds_bpermute(
+                                                   src << 2, __float_as_int(b.sar[t])));
                         } else {
                             tv[t] = FT ? gather_few(b.tl[u][t][0]) : gather(b.tl[u][t]);
                             sa[t] = __int_as_float(
@@ -1943,9 +1948,15 @@ void skinny_launch(dim3 g, size_t shm, hipStream_t s, const void* av) {
     const KArgs& a = *(const KArgs*)av;
     constexpr int kFewTok = NT == 1 && NW <= 2 ? kSkinnyFewTokens : 0;
     constexpr int kOneTok = NT == 1 ? kSkinnyOneToken : 0;
+    // direct token loads at M <= 2 with row-major B, where the tokens' and
+    // the weights' ds_bpermute bound the call (7-15% faster warm at M = 1 and
+    // 2 on the larger decode shapes, within 3% cold); at M = 4 their extra L1
+    // accesses already cost as much as they save, and with a shuffled B
+    // (no weight gather left) at any M
+    constexpr int kDirectTokensMax = BM == kSkinnyBShuf ? 0 : 2;
     if (a.split_last)
         hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kSkinnyLast>), g, dim3(64 * S), shm, s, a);
-    else if (kOneTok && a.M == 1)
+    else if (kOneTok && a.M <= kDirectTokensMax)
         hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kOneTok>), g, dim3(64 * S), shm, s, a);
     else if (kFewTok && a.M <= 8)
         hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kFewTok>), g, dim3(64 * S), shm, s, a);
