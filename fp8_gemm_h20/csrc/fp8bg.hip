@@ -1279,7 +1279,7 @@ void fp8bg_ring_dp_bs(KArgs a) {
 // of a 16-row block's 128-K group are stored in MFMA lane order, so lane l's
 // loads at bytes 16 l and 1024 + 16 l of the block are its operand as they
 // arrive, and the weights need no ds_bpermute.
-// kSkinnyOneToken: fp8 tokens loaded in the MFMA layout, for launches with at
+// kSkinnyDirectTokens: fp8 tokens loaded in the MFMA layout, for launches with at
 // most two tokens and row-major B (see the skinny launcher).  Rows of the 16-token operand at or past M
 // reach no stored output, so lane (r, q) loads row min(r, M - 1)'s chunks q
 // and 4 + q itself and the tokens need no ds_bpermute; with one token its
@@ -1287,7 +1287,7 @@ void fp8bg_ring_dp_bs(KArgs a) {
 // row's scale comes by ds_bpermute as in the general path.  Bitwise the same
 // C as the general path.
 constexpr int kSkinnyQuant = 1, kSkinnyLast = 2, kSkinnyQuantFew = 4, kSkinnyFewTokens = 8,
-              kSkinnyBShuf = 16, kSkinnyOneToken = 32;
+              kSkinnyBShuf = 16, kSkinnyDirectTokens = 32;
 template <int NWB, int NTB, int S, int U, int MODE>
 __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     constexpr int TW = 16 * NWB, TT = 16 * NTB, NB = NWB * NTB;
@@ -1295,8 +1295,8 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     constexpr bool QF = MODE & kSkinnyQuantFew;
     constexpr bool FT = MODE & kSkinnyFewTokens;
     constexpr bool BSH = MODE & kSkinnyBShuf;
-    constexpr bool OT = MODE & kSkinnyOneToken;
-    static_assert(!OT || (!QA && !FT && NTB == 1), "the one-token load takes one 16-token tile of fp8 tokens");
+    constexpr bool DT = MODE & kSkinnyDirectTokens;
+    static_assert(!DT || (!QA && !FT && NTB == 1), "the direct token load takes one 16-token tile of fp8 tokens");
     static_assert(!QF || (QA && NTB == 1), "the few-token quantiser takes one 16-token tile");
     static_assert(!FT || (!QA && NTB == 1), "the few-token load takes one 16-token tile of fp8 tokens");
     __shared__ f32x4 red[S][NB][64];
@@ -1365,7 +1365,7 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
             xp[t] = a.X + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.ldx + 16 * lc;
         } else {
             // (the launch's only token tile starts at row 0)
-            tp[t] = OT   ? a.A + (size_t)min(r, a.M - 1) * a.K + 16 * q
+            tp[t] = DT   ? a.A + (size_t)min(r, a.M - 1) * a.K + 16 * q
                     : FT ? a.A + (size_t)min(t0 + (lane >> 3), a.M - 1) * a.K + 16 * (lane & 7)
                          : a.A + (size_t)min(t0 + 16 * t + lr, a.M - 1) * a.K + 16 * lc;
             asp[t] = a.As + (int64_t)min(t0 + 16 * t + sa_row, a.M - 1) * a.as_sm;
@@ -1580,7 +1580,7 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                         sa[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(op_src, __float_as_int(b.sa[u][t])));
                     } else {
                         const int src = as_cm ? r + 16 * u : 4 * r + u;
-                        if constexpr (OT) {
+                        if constexpr (DT) {
                             // one token: slot u of row 0 sits in lane 16 u
                             // (column-major As) or u
                             tv[t] = (i32x8){b.tl[u][t][0][0], b.tl[u][t][0][1], b.tl[u][t][0][2],
@@ -1947,7 +1947,7 @@ template <int NW, int NT, int S, int U, int BM>
 void skinny_launch(dim3 g, size_t shm, hipStream_t s, const void* av) {
     const KArgs& a = *(const KArgs*)av;
     constexpr int kFewTok = NT == 1 && NW <= 2 ? kSkinnyFewTokens : 0;
-    constexpr int kOneTok = NT == 1 ? kSkinnyOneToken : 0;
+    constexpr int kDirectTok = NT == 1 ? kSkinnyDirectTokens : 0;
     // direct token loads at M <= 2 with row-major B, where the tokens' and
     // the weights' ds_bpermute bound the call (7-15% faster warm at M = 1 and
     // 2 on the larger decode shapes, within 3% cold); at M = 4 their extra L1
@@ -1956,8 +1956,8 @@ void skinny_launch(dim3 g, size_t shm, hipStream_t s, const void* av) {
     constexpr int kDirectTokensMax = BM == kSkinnyBShuf ? 0 : 2;
     if (a.split_last)
         hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kSkinnyLast>), g, dim3(64 * S), shm, s, a);
-    else if (kOneTok && a.M <= kDirectTokensMax)
-        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kOneTok>), g, dim3(64 * S), shm, s, a);
+    else if (kDirectTok && a.M <= kDirectTokensMax)
+        hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kDirectTok>), g, dim3(64 * S), shm, s, a);
     else if (kFewTok && a.M <= 8)
         hipLaunchKernelGGL((fp8bg_skinny<NW, NT, S, U, BM | kFewTok>), g, dim3(64 * S), shm, s, a);
     else
