@@ -45,6 +45,7 @@ def mfma_rate(torch, device, stream, iters=4096, workgroups_per_cu=2, reps=5, pr
     scale = torch.ones(64, dtype=torch.float32, device=device)
     out = torch.empty(wgs * 256, dtype=torch.float32, device=device)
     name = "fp8bg_calib_mfma_promoted" if promoted else "fp8bg_calib_mfma"
+    stream.wait_stream(torch.cuda.current_stream(device))    # the fills above come first
 
     def launch():
         if promoted:
@@ -71,6 +72,7 @@ def read_rate(torch, device, stream, nbytes=1 << 30, workgroups_per_cu=2, reps=5
     wgs = _num_cus(device) * workgroups_per_cu
     buf = torch.ones(nbytes // 4, dtype=torch.int32, device=device)
     out = torch.empty(wgs * 256, dtype=torch.int32, device=device)
+    stream.wait_stream(torch.cuda.current_stream(device))    # the fill above comes first
 
     def launch():
         _lib.check(lib.fp8bg_calib_read(buf.data_ptr(), buf.numel() * 4, out.data_ptr(), wgs,
@@ -90,6 +92,7 @@ def write_rate(torch, device, stream, nbytes=1 << 30, workgroups_per_cu=2, reps=
     wgs = _num_cus(device) * workgroups_per_cu
     buf = torch.zeros(nbytes // 4, dtype=torch.int32, device=device)
     value = 0x3F803F80                               # two bf16 1.0
+    stream.wait_stream(torch.cuda.current_stream(device))    # the zero fill comes first
 
     def launch():
         _lib.check(lib.fp8bg_calib_write(buf.data_ptr(), buf.numel() * 4, value, wgs,
