@@ -11,7 +11,7 @@ from pathlib import Path
 
 LIB_NAME = "libfp8bg.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 OK = 0
 ERR_SHAPE = 1
@@ -34,6 +34,7 @@ SPLIT_NONE = 0
 SPLIT_TAIL = 1
 SPLIT_FULL = 2
 SPLIT_LAST = 3
+SPLIT_STREAM = 4
 
 # uint32 tile counters at the start of every split-K workspace (FP8BG_COUNTERS)
 COUNTERS = 4096
@@ -99,6 +100,7 @@ class Plan(ctypes.Structure):
         ("lds_bytes", ctypes.c_int32),
         ("threads", ctypes.c_int32),
         ("kernel_id", ctypes.c_int32),
+        ("stream_units", ctypes.c_int32),
     ]
 
 

@@ -107,9 +107,10 @@ struct KArgs {
     const uint16_t* bias;  // [N] bf16 or nullptr
     float* ws;             // split-K partials [split tile][split][tt][tw]
                            // (FP8BG_SPLIT_LAST: [split tile][split][block][lane] f32x4)
-    uint32_t* cnt;         // FP8BG_SPLIT_LAST tile counters (zero between calls)
+    uint32_t* cnt;         // FP8BG_SPLIT_LAST / _STREAM tile counters (zero between calls)
     int split_last;        // split tiles reduced in the GEMM kernel (selects its instance)
-    int kcount;            // 128-K groups per workgroup: K / 128 / split
+    int kcount;            // 128-K groups per workgroup: K / 128 / split (stream-K:
+                           // the units, tile x group, of each workgroup's run)
     uint2 div_split;       // fast_div reciprocals of split and tiles_t
     uint2 div_tiles_t;
     int64_t as_sm, as_sk, bs_sn, bs_sk;
@@ -129,6 +130,7 @@ struct KArgs {
     uint8_t* q_out;        // optional [M, K] e4m3 copy of the quantised activations
     float* s_out;          // optional [M, K/128] scales, strides qs_sm, qs_sk
     int64_t qs_sm, qs_sk;
+    int stream;            // stream-K launch (FP8BG_SPLIT_STREAM; selects its instance)
 };
 
 // Two fp32 -> packed bf16 with gfx950's v_cvt_pk_bf16_f32: round to nearest
@@ -567,12 +569,30 @@ constexpr bool ring_has_dp(int TW, int TT, int KF, int KU, int WK) {
 // decode and small-M sizes, where few tiles leave most CUs idle.
 constexpr bool ring_has_last(int TT, int KF) { return TT <= 64 && KF == 0; }
 
+// Whether a ring instance also has an fp8bg_ring_sk kernel (stream-K,
+// FP8BG_SPLIT_STREAM): one K slice, a runtime K loop, and accumulators
+// ((TW / WW) x (TT / WT) / 64 VGPRs per wave) that leave room for the two
+// more sets of them the fixup loads: at most 64 with two waves per SIMD or
+// fewer, 32 with three (larger ones spill).
+constexpr bool ring_has_sk(int TW, int TT, int WW, int WT, int KF, int WK) {
+    return KF == 0 && WK == 1 && (TW / WW) * (TT / WT) / 64 <= (WW * WT > 8 ? 32 : 64);
+}
+
 // The ring kernel's body.  DPO: every workgroup of the launch is a whole
 // (data-parallel) tile, none computes a K split.  BSH: B in the shuffled
 // layout (kShufBlock); its 16-row blocks reach LDS in MFMA lane order, so
 // each wave reads a weight operand as two lane-linear 16-byte loads.
+// SK: stream-K (FP8BG_SPLIT_STREAM).  The launch's tiles x K-groups units
+// are dealt out in equal contiguous runs of a.kcount units, one run per
+// workgroup (per <= K/128: a run touches at most two tiles).  The ring runs
+// straight through the run: the loads of the second tile's first groups are
+// issued while the first tile's last groups compute, so the pipeline never
+// drains between them.  A run that starts inside tile a and ends inside
+// tile a + 1 computes tile a + 1's head first and tile a's tail last; the
+// workgroup holding a tile's tail owns it and, finishing last, normally
+// finds the other parts of the tile stored already.
 template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK, bool DPO, bool LAST,
-          bool BSH = false>
+          bool BSH = false, bool SK = false>
 __device__ __forceinline__ void ring_body(const KArgs& a) {
     constexpr int NWAVE = WW * WT;                // waves of one K slice
     constexpr int WTW = TW / WW;
@@ -614,7 +634,30 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
     const int KG = KF ? KF : (a.K / kGroupK);
     int pid = blockIdx.x;
     int tile, sidx = 0, kcount, k_lo;
-    if (pid < a.n_dp) {
+    // stream-K: the workgroup's place in the unit order (sk_w), the units of
+    // the tile it computes first (n1; kcount when the run stays in one
+    // tile), and the tile it computes second with that tile's first group
+    int sk_w = 0, n1 = 0, tile2 = 0, k_lo2 = 0;
+    if constexpr (SK) {
+        static_assert(ring_has_sk(TW, TT, WW, WT, KF, WK), "stream-K instance");
+        sk_w = a.xcd_remap ? xcd_remap(pid, (int)gridDim.x) : pid;
+        const int u0 = sk_w * a.kcount;
+        const int u1 = min(u0 + a.kcount, a.tiles_w * a.tiles_t * KG);
+        const int ta = u0 / KG, tb = (u1 - 1) / KG;
+        kcount = u1 - u0;
+        if (ta == tb) {
+            tile = ta;
+            k_lo = u0 - ta * KG;
+            n1 = kcount;
+        } else {
+            // tile tb's head (groups 0 .. n1 - 1) first, then tile ta's tail
+            tile = tb;
+            k_lo = 0;
+            n1 = u1 - tb * KG;
+            tile2 = ta;
+            k_lo2 = u0 - ta * KG;
+        }
+    } else if (pid < a.n_dp) {
         if (a.xcd_remap) pid = xcd_remap(pid, a.n_dp);
         tile = pid;
         k_lo = 0;
@@ -628,6 +671,11 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
     }
     int w0, t0;
     tile_origin(tile, a, w0, t0);
+    int w0b = w0, t0b = t0;                       // stream-K: the second tile's origin
+    if (SK && n1 < kcount) tile_origin(tile2, a, w0b, t0b);
+    // weight origin of the tile being computed (its Bs block), changed
+    // between a stream-K run's two tiles
+    int w0c = w0;
 
     // ---- DMA sources: operand block b holds rows 8b .. 8b+7; wave w moves
     // blocks w * NJ .. w * NJ + NJ - 1.  When the NBLK blocks do not divide
@@ -647,33 +695,38 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
     // tile's 16-row block b / 2, copied as it lies, 16 bytes per lane)
     bool from_b[NJ];
     uint32_t soff[NJ];
+    uint32_t soff2[SK ? NJ : 1];                  // stream-K: the second tile's
     int dblk[NJ];
+    auto op_off = [&](int j, int w0_, int t0_) -> uint32_t {
+        const int b = dblk[j];
+        const int row = 8 * b + (lane >> 3);
+        const int chunk = (lane & 7) ^ swz_ring(row, a.swz);
+        if (from_b[j] && BSH)
+            return (uint32_t)min((w0_ >> 4) + (b >> 1), (a.N >> 4) - 1) * (uint32_t)(a.K / kGroupK) *
+                       (uint32_t)kShufBlock +
+                   (b & 1) * (kShufBlock / 2) + shuf_slot(lane) * 16;
+        if (from_b[j]) return (uint32_t)min(w0_ + row, a.N - 1) * (uint32_t)a.K + chunk * 16;
+        return (uint32_t)min(t0_ + row - TW, a.M - 1) * (uint32_t)a.K + chunk * 16;
+    };
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const int b_raw = wave * NJ + j;
         const int b = b_raw < NBLK ? b_raw : b_raw - NBLK;
         dblk[j] = b;
-        const int row = 8 * b + (lane >> 3);
-        const int chunk = (lane & 7) ^ swz_ring(row, a.swz);
         from_b[j] = 8 * b < TW;                   // wave-uniform
-        if (from_b[j] && BSH)
-            soff[j] = (uint32_t)min((w0 >> 4) + (b >> 1), (a.N >> 4) - 1) * (uint32_t)(a.K / kGroupK) *
-                          (uint32_t)kShufBlock +
-                      (b & 1) * (kShufBlock / 2) + shuf_slot(lane) * 16;
-        else if (from_b[j])
-            soff[j] = (uint32_t)min(w0 + row, a.N - 1) * (uint32_t)a.K + chunk * 16;
-        else
-            soff[j] = (uint32_t)min(t0 + row - TW, a.M - 1) * (uint32_t)a.K + chunk * 16;
+        soff[j] = op_off(j, w0, t0);
+        if constexpr (SK) soff2[j] = op_off(j, w0b, t0b);
     }
     // scale slot q = 64 * (h * NWAVE + wave) + lane of slice h: As of token
     // t0 + q, then Bs of weight block w0 / 128 + (q - TT) for the NBS blocks
     // the tile spans, then bias dword (q - TT - NBS) = columns w0 + 2 (q - TT
     // - NBS) and the next one (the same every group); spare slots, and the
-    // bias slots without a bias, reload As[0, g] (never read)
+    // bias slots without a bias, reload As[0, g] (never read).  Stream-K
+    // adds the bias where it writes C, from global memory.
     const float* sc_base[NSC];
+    const float* sc_base2[SK ? NSC : 1];
     int64_t sc_step[NSC];
-#pragma unroll
-    for (int h = 0; h < NSC; ++h) {
+    auto sc_src = [&](int h, int w0_, int t0_) -> const float* {
         const int q = 64 * (h * NWAVE + wave) + lane;
         if (q < TT) {
             // slot r * NT + t of a wave's WTT-token range holds token
@@ -681,31 +734,45 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
             // block) are contiguous, one or two 16-byte reads per group
             const int ql = q % WTT;
             const int tok = q - ql + (ql % NT) * 16 + ql / NT;
-            sc_base[h] = a.As + (int64_t)min(t0 + tok, a.M - 1) * a.as_sm;
-            sc_step[h] = a.as_sk;
-        } else if (q < TT + NBS) {
-            sc_base[h] = a.Bs + (int64_t)min(w0 / 128 + (q - TT), a.N / 128 - 1) * a.bs_sn;
-            sc_step[h] = a.bs_sk;
-        } else if (q < TT + NBS + TW / 2 && a.bias) {
-            sc_base[h] = (const float*)(a.bias + min(w0 + 2 * (q - TT - NBS), a.N - 2));
-            sc_step[h] = 0;
-        } else {
-            sc_base[h] = a.As;
-            sc_step[h] = a.as_sk;
+            return a.As + (int64_t)min(t0_ + tok, a.M - 1) * a.as_sm;
         }
+        if (q < TT + NBS) return a.Bs + (int64_t)min(w0_ / 128 + (q - TT), a.N / 128 - 1) * a.bs_sn;
+        if (!SK && q < TT + NBS + TW / 2 && a.bias)
+            return (const float*)(a.bias + min(w0_ + 2 * (q - TT - NBS), a.N - 2));
+        return a.As;
+    };
+#pragma unroll
+    for (int h = 0; h < NSC; ++h) {
+        const int q = 64 * (h * NWAVE + wave) + lane;
+        sc_base[h] = sc_src(h, w0, t0);
+        if constexpr (SK) sc_base2[h] = sc_src(h, w0b, t0b);
+        sc_step[h] = q < TT ? a.as_sk : q < TT + NBS ? a.bs_sk : (!SK && q < TT + NBS + TW / 2 && a.bias) ? 0 : a.as_sk;
     }
+    // g: the 128-K group of the tile (stream-K: the unit of the run, in the
+    // order the run computes them, the second tile's from n1 on)
     auto dma_block = [&](int j, int g, int stage) {
+        uint32_t off = soff[j];
+        if constexpr (SK) {
+            const bool second = g >= n1;          // wave-uniform
+            off = second ? soff2[j] : soff[j];
+            g = second ? k_lo2 + (g - n1) : k_lo + g;
+        }
         __builtin_amdgcn_raw_ptr_buffer_load_lds(from_b[j] ? rsB : rsA,
                                                  FP8BG_LDS_PTR(lds + stage * STAGE + dblk[j] * 1024), 16,
-                                                 soff[j],
+                                                 off,
                                                  (uint32_t)g * (BSH && from_b[j] ? kShufBlock : kGroupK), 0,
                                                  0);
     };
     auto dma_scales = [&](int g, int stage) {
+        bool second = false;
+        if constexpr (SK) {
+            second = g >= n1;
+            g = second ? k_lo2 + (g - n1) : k_lo + g;
+        }
 #pragma unroll
         for (int h = 0; h < NSC; ++h)
             __builtin_amdgcn_global_load_lds(
-                (const void*)(sc_base[h] + (int64_t)g * sc_step[h]),
+                (const void*)((SK && second ? sc_base2[h] : sc_base[h]) + (int64_t)g * sc_step[h]),
                 FP8BG_LDS_PTR(lds + stage * STAGE + OPS + (h * NWAVE + wave) * 256), 4, 0, 0);
     };
     auto dma = [&](int g, int stage) {
@@ -753,7 +820,9 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
     // step's loads would all be clamped; it is peeled off without them (no
     // wait counts the loads issued after the ones it waits for).
     const int g_last = k_lo + kcount - 1;
-    for (int s = ks; s < ST - KU; s += WK) dma(min(k_lo + s, g_last), s);
+    // the group (stream-K: the unit of the run) that step slot v loads
+    auto load_idx = [&](int v) { return SK ? min(v, kcount - 1) : min(k_lo + v, g_last); };
+    for (int s = ks; s < ST - KU; s += WK) dma(load_idx(s), s);
 
     // One 128-K group: stage i % ST is computed while the loads of group
     // g_next are spread over its token blocks (operand block j before token
@@ -788,7 +857,7 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
             wop[w] = wread(st, wv_w * WTW + w * 16);
             __builtin_amdgcn_sched_barrier(0);
         }
-        const float sb = sc[TT + (w0 % 128 + wv_w * WTW) / 128];
+        const float sb = sc[TT + (w0c % 128 + wv_w * WTW) / 128];
         float sa[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) sa[t] = sc[wv_t * WTT + (lane & 15) * NT + t];
@@ -877,7 +946,7 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
         i32x8 wop[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) wop[w] = wread(st, wv_w * WTW + w * 16);
-        const float sb = sc[TT + (w0 % 128 + wv_w * WTW) / 128];
+        const float sb = sc[TT + (w0c % 128 + wv_w * WTW) / 128];
         const int r = lane & 15, qd = lane >> 4;
         // byte offsets of the lane's C chunks inside a 16-row block
         constexpr int HC = (16 * CPR + 63) / 64;
@@ -970,16 +1039,146 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
             const int u = uk * WK + ks;
             const int g = i + ST - KU + u;
             if (decltype(first)::value && uk == 0)
-                group(i + u, min(k_lo + g, g_last), g % ST, role, load, First<true>{});
+                group(i + u, load_idx(g), g % ST, role, load, First<true>{});
             else
-                group(i + u, min(k_lo + g, g_last), g % ST, role, load, First<false>{});
+                group(i + u, load_idx(g), g % ST, role, load, First<false>{});
         }
     };
+    // Stream-K: the end of one tile's part of a run (groups g_begin ..
+    // g_end - 1 of tile tile_), per wave.  A part covering the whole tile
+    // writes C.  Otherwise the tile's parts come from consecutive runs (2 or
+    // 3: the host keeps a run at least half a tile long), and the part
+    // holding the tile's last group is the owner.  Every other part stores
+    // its fp32 partial with device-scope stores (coherent across the XCDs'
+    // L2s), waits for them and counts itself in the tile's per-wave counter.
+    // The owner first reads the counter: when all the other parts are
+    // counted it sums the tile without storing its own partial; otherwise it
+    // stores and counts itself too, and the part whose count completes the
+    // tile sums it.  The sum runs in K order over the parts (each part's
+    // value from its partial, or its own registers), so C does not depend on
+    // which part sums; that part writes C with the bias and resets the
+    // counter.  No wave waits for another.  Partial slots: 2 w + 1 holds the
+    // part of run w that is its second tile's head, 2 w the other part.
+    auto sk_finish = [&](int tile_, int w0_, int t0_, int g_begin, int g_end, int own_slot)
+        __attribute__((always_inline)) {
+        const int r = lane & 15, qd = lane >> 4;
+        auto write_c = [&]() {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int w = 0; w < NW; ++w) {
+                    const int m = t0_ + wv_t * WTT + t * 16 + r, n = w0_ + wv_w * WTW + w * 16 + qd * 4;
+                    if (m < a.M && n < a.N) *(uint2*)(a.C + (size_t)m * a.N + n) = out_bf16x4(acc[w][t], a.bias, n);
+                }
+        };
+        if (g_begin == 0 && g_end == KG) {
+            write_c();
+            return;
+        }
+        const int tkg = tile_ * KG;
+        const int wa = tkg / a.kcount, wb = (tkg + KG - 1) / a.kcount;
+        const int parts = wb - wa + 1;            // 2 or 3
+        const int pos = sk_w - wa;                // this part's place in K order
+        const uint32_t others = (uint32_t)(parts - 1);
+        const __amdgpu_buffer_rsrc_t wrs =
+            __builtin_amdgcn_make_buffer_rsrc((void*)a.ws, (short)0, 0x7fffffff, kBufferFlags);
+        auto part_off = [&](int slot, int w, int t) -> uint32_t {
+            return ((((uint32_t)slot * NWAVE + wave) * (NW * NT) + (uint32_t)(w * NT + t)) * 64u + lane) * 16u;
+        };
+        auto store_part = [&]() {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int w = 0; w < NW; ++w)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[w][t]), wrs,
+                                                           part_off(own_slot, w, t), 0, kDeviceScope);
+            asm volatile("" ::: "memory");
+            wait_vmcnt<0>();
+            asm volatile("" ::: "memory");
+        };
+        uint32_t* cnt = a.cnt + tile_ * NWAVE + wave;
+        uint32_t seen = 0;
+        bool sum_here;
+        if (g_end == KG) {
+            if (lane == 0) seen = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sum_here = __builtin_amdgcn_readfirstlane(seen) == others;
+            if (!sum_here) {
+                store_part();
+                if (lane == 0) seen = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                sum_here = __builtin_amdgcn_readfirstlane(seen) == others;
+            }
+        } else {
+            store_part();
+            if (lane == 0) seen = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sum_here = __builtin_amdgcn_readfirstlane(seen) == others;
+        }
+        if (!sum_here) return;
+        asm volatile("" ::: "memory");
+        // the other parts in K order: o0, then o1 (three parts)
+        const int p0 = pos == 0 ? 1 : 0, p1 = pos <= 1 ? 2 : 1;
+        auto slot_of = [&](int p) { return 2 * (wa + p) + (p == 0 && wa * a.kcount < tkg ? 1 : 0); };
+        const int s0 = slot_of(p0), s1 = slot_of(p1);
+        f32x4 o0[NW][NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+                o0[w][t] = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, part_off(s0, w, t), 0, kDeviceScope));
+        if (parts == 3) {
+            f32x4 o1[NW][NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int w = 0; w < NW; ++w)
+                    o1[w][t] = __builtin_bit_cast(
+                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, part_off(s1, w, t), 0, kDeviceScope));
+            // (P0 + P1) + P2, with this part's own value in its place
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int w = 0; w < NW; ++w) {
+                    if (pos == 2)
+                        acc[w][t] = (o0[w][t] + o1[w][t]) + acc[w][t];
+                    else
+                        acc[w][t] = (acc[w][t] + o0[w][t]) + o1[w][t];
+                }
+        } else {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int w = 0; w < NW; ++w) acc[w][t] = acc[w][t] + o0[w][t];
+        }
+        write_c();
+        if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+
     // The last step is peeled off outside the loop (a second copy inside the
     // loop body would make the large tiles spill).
     // a uniform branch around two copies of the loop, so the priority
     // switches are immediates inside straight-line code
-    if constexpr (kEarlyC) {
+    if constexpr (SK) {
+        // the first tile's steps, its part's end, then the second tile's
+        // steps; the ring's loads run on across the tiles (load_idx counts
+        // the run's units)
+        if (kcount > KU) {
+            step(0, WaveRole<0>{}, Loads<true>{}, First<true>{});
+            int i = KU;
+            for (; i < n1 && i + KU < kcount; i += KU) step(i, WaveRole<0>{}, Loads<true>{}, First<false>{});
+            if (n1 < kcount) {
+                sk_finish(tile, w0, t0, 0, n1, 2 * sk_w + 1);
+#pragma unroll
+                for (int w = 0; w < NW; ++w)
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) acc[w][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                w0c = w0b;
+                for (; i + KU < kcount; i += KU) step(i, WaveRole<0>{}, Loads<true>{}, First<false>{});
+            }
+            step(kcount - KU, WaveRole<0>{}, Loads<false>{}, First<false>{});
+        } else {
+            step(0, WaveRole<0>{}, Loads<false>{}, First<true>{});
+        }
+    } else if constexpr (kEarlyC) {
         // the last step is dispatched after the loop, and the C-writing one
         // returns right away (a path that rejoined the epilogue would keep
         // the epilogue's registers alive through it)
@@ -1034,6 +1233,13 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
     // The clamped loads of the last ST - 2 KU groups are still in flight: they
     // must land before the LDS is reused below or handed to another workgroup.
     wait_vmcnt<0>();
+    if constexpr (SK) {
+        if (n1 < kcount)
+            sk_finish(tile2, w0b, t0b, k_lo2, KG, 2 * sk_w);
+        else
+            sk_finish(tile, w0, t0, k_lo, k_lo + kcount, 2 * sk_w);
+        return;
+    }
 
     // ---- epilogue ----
     const bool dp = blockIdx.x < a.n_dp;
@@ -1219,6 +1425,20 @@ __global__ __launch_bounds__(64 * WW * WT * WK)
 __attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
 void fp8bg_ring_dp(KArgs a) {
     ring_body<TW, TT, WW, WT, ST, KF, KU, WK, true, false>(a);
+}
+
+// Stream-K (FP8BG_SPLIT_STREAM), for the instances ring_has_sk names.
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK>
+__global__ __launch_bounds__(64 * WW * WT * WK)
+__attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
+void fp8bg_ring_sk(KArgs a) {
+    ring_body<TW, TT, WW, WT, ST, KF, KU, WK, false, false, false, true>(a);
+}
+template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK>
+__global__ __launch_bounds__(64 * WW * WT * WK)
+__attribute__((amdgpu_waves_per_eu((WW * WT * WK + 3) / 4, (WW * WT * WK + 3) / 4)))
+void fp8bg_ring_sk_bs(KArgs a) {
+    ring_body<TW, TT, WW, WT, ST, KF, KU, WK, false, false, true, true>(a);
 }
 
 // The three ring kernels for a shuffled B (FP8BG_FLAG_B_SHUFFLED).
@@ -1991,6 +2211,15 @@ template <int TW, int TT, int WW, int WT, int ST, int KF, int KU, int WK, bool B
 void ring_launch(dim3 g, size_t shm, hipStream_t s, const void* av) {
     const KArgs& a = *(const KArgs*)av;
     const dim3 block(64 * WW * WT * WK);
+    if constexpr (ring_has_sk(TW, TT, WW, WT, KF, WK)) {
+        if (a.stream) {
+            if constexpr (BSH)
+                hipLaunchKernelGGL((fp8bg_ring_sk_bs<TW, TT, WW, WT, ST, KF, KU, WK>), g, block, shm, s, a);
+            else
+                hipLaunchKernelGGL((fp8bg_ring_sk<TW, TT, WW, WT, ST, KF, KU, WK>), g, block, shm, s, a);
+            return;
+        }
+    }
     if constexpr (ring_has_last(TT, KF)) {
         if (a.split_last) {
             if constexpr (BSH)
@@ -2324,7 +2553,7 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     const int ki = find_instance(cfg);
     if (ki < 0) return FP8BG_ERR_CONFIG;
     if (cfg->split < 1 || cfg->group_t < 1 || num_cus < 1) return FP8BG_ERR_CONFIG;
-    if (cfg->split_mode < FP8BG_SPLIT_NONE || cfg->split_mode > FP8BG_SPLIT_LAST) return FP8BG_ERR_CONFIG;
+    if (cfg->split_mode < FP8BG_SPLIT_NONE || cfg->split_mode > FP8BG_SPLIT_STREAM) return FP8BG_ERR_CONFIG;
     if (cfg->flags & ~(FP8BG_FLAG_SCALE_LDS | FP8BG_FLAG_XCD_REMAP | FP8BG_FLAG_SWZ8 |
                        FP8BG_FLAG_SWZPAIR | FP8BG_FLAG_B_SHUFFLED))
         return FP8BG_ERR_CONFIG;
@@ -2342,7 +2571,9 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
                  (int64_t)N * 32 > 0x7fffffffLL))
         return FP8BG_ERR_SHAPE;
 
-    int split = (cfg->split_mode == FP8BG_SPLIT_NONE || k.kf) ? 1 : cfg->split;
+    const bool stream = cfg->split_mode == FP8BG_SPLIT_STREAM;
+    if (stream && !(ring && ring_has_sk(k.tw, k.tt, k.ww, k.wt, k.kf, k.wk))) return FP8BG_ERR_CONFIG;
+    int split = (cfg->split_mode == FP8BG_SPLIT_NONE || k.kf || stream) ? 1 : cfg->split;
     if (kg % split) split = 1;  // reference baseline_gluon.py:274-276
     const bool last = cfg->split_mode == FP8BG_SPLIT_LAST;
     if (last && !skinny && !(ring && ring_has_last(k.tt, k.kf))) return FP8BG_ERR_CONFIG;
@@ -2364,9 +2595,34 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     // a ring kernel computing KU groups per barrier needs whole multiples of
     // KU in every workgroup's K range (kg / split divides kg)
     if (ring && (kg / split) % k.unroll) return FP8BG_ERR_CONFIG;
-    const int64_t n_dp = tiles - n_split;
-    const int64_t grid = n_dp + n_split * split;
+    int64_t n_dp = tiles - n_split;
+    int64_t grid = n_dp + n_split * split;
     if (grid > 0x7fffffff) return FP8BG_ERR_SHAPE;
+    // Stream-K: tiles x K-groups units dealt out in runs of `per` units, one
+    // run per workgroup, about one run per CU.  A run is at least half a tile
+    // (so at most three runs share a tile) and at most one tile less a group
+    // (so it touches at most two tiles); a multiple of the groups per
+    // barrier.  Where that leaves no tile cut (tiles >= CUs), or the
+    // counters (one per tile and wave) or the partials' 31-bit offsets do
+    // not fit, the launch runs whole tiles instead, so a table entry of this
+    // mode stays valid at any M.
+    int64_t stream_units = 0, ws_stream = 0;
+    if (stream) {
+        const int ku = k.unroll;
+        const int64_t units = tiles * kg;
+        int64_t per = (units + num_cus - 1) / num_cus;
+        per = max(per, (int64_t)(kg / 2));
+        per = (per + ku - 1) / ku * ku;
+        const int64_t sk_grid = (units + per - 1) / per;
+        const int64_t parts = 2 * sk_grid * (int64_t)k.tw * k.tt;
+        if (per < kg && tiles * k.ww * k.wt <= FP8BG_COUNTERS && parts * 4 <= 0x7fffffffLL) {
+            stream_units = per;
+            ws_stream = FP8BG_COUNTERS + parts;
+            n_dp = 0;
+            n_split = tiles;
+            grid = sk_grid;
+        }
+    }
     int64_t lds;
     if (skinny) {
         lds = (int64_t)k.wk * (k.tw / 16) * (k.tt / 16) * 64 * 16;
@@ -2387,11 +2643,14 @@ int fp8bg_make_plan(int32_t M, int32_t N, int32_t K, const fp8bg_config* cfg, in
     plan->n_dp = (int32_t)n_dp;
     plan->n_split = (int32_t)n_split;
     plan->grid = (int32_t)grid;
-    plan->launches = n_split && !in_kernel ? 2 : 1;
-    plan->ws_elems = n_split ? FP8BG_COUNTERS + n_split * split * (int64_t)k.tw * k.tt : 0;
+    plan->launches = n_split && !in_kernel && !stream_units ? 2 : 1;
+    plan->ws_elems = stream_units ? ws_stream
+                     : n_split    ? FP8BG_COUNTERS + n_split * split * (int64_t)k.tw * k.tt
+                                  : 0;
     plan->lds_bytes = (int32_t)lds;
     plan->threads = k.threads;
     plan->kernel_id = ki;
+    plan->stream_units = (int32_t)stream_units;
     return FP8BG_OK;
 }
 
@@ -2431,7 +2690,8 @@ int gemm_enqueue(const void* A, const void* B, const float* As, int64_t as_strid
     // workspace: the tile counters, then the partials
     a.cnt = (uint32_t*)ws;
     a.ws = ws ? ws + FP8BG_COUNTERS : nullptr;
-    a.split_last = p.n_split > 0 && p.launches == 1;  // FP8BG_SPLIT_LAST within its limits
+    a.stream = p.stream_units > 0;
+    a.split_last = p.n_split > 0 && p.launches == 1 && !a.stream;  // FP8BG_SPLIT_LAST within its limits
     a.as_sm = as_stride_m;
     a.as_sk = as_stride_k;
     a.bs_sn = bs_stride_n;
@@ -2445,7 +2705,7 @@ int gemm_enqueue(const void* A, const void* B, const float* As, int64_t as_strid
     a.tiles_t = p.tiles_t;
     a.n_dp = p.n_dp;
     a.split = p.split;
-    a.kcount = (K / kGroupK) / p.split;
+    a.kcount = a.stream ? p.stream_units : (K / kGroupK) / p.split;
     a.div_split = fast_div_of((uint32_t)p.split);
     a.div_tiles_t = fast_div_of((uint32_t)p.tiles_t);
     a.group_t = cfg->group_t;
@@ -2456,7 +2716,7 @@ int gemm_enqueue(const void* A, const void* B, const float* As, int64_t as_strid
     hipStream_t s = (hipStream_t)stream;
     ((cfg->flags & FP8BG_FLAG_B_SHUFFLED) ? k.launch_bs : k.launch)(dim3(p.grid), shm, s, &a);
     if (hipGetLastError() != hipSuccess) return FP8BG_ERR_LAUNCH;
-    if (p.n_split > 0 && !a.split_last) {
+    if (p.launches == 2) {
         const int parts = reduce_parts(p, k, num_cus);
         hipLaunchKernelGGL(fp8bg_split_reduce, dim3(p.n_split * parts), dim3(kThreads), 0, s, a,
                            k.kind == FP8BG_KIND_SKINNY ? 1 : 0, parts);

@@ -109,8 +109,13 @@ RING = (
 # SPLIT_MODE "last"): token tiles up to 64, no fixed K; must match
 # ring_has_last in csrc/fp8bg.hip
 RING_LAST = tuple(c for c in RING if c[1] <= 64 and c[5] == 0)
+# ring instances with a stream-K kernel (fp8bg_ring_sk, SPLIT_MODE "stream"):
+# no fixed K, one K slice, and at most 64 accumulator VGPRs per wave (32 with
+# more than 8 waves); must match ring_has_sk in csrc/fp8bg.hip
+RING_SK = tuple(c for c in RING if c[5] == 0 and c[7] == 1
+                and (c[0] // c[2]) * (c[1] // c[3]) // 64 <= (32 if c[2] * c[3] > 8 else 64))
 SPLIT_MODES = {"none": _lib.SPLIT_NONE, "tail": _lib.SPLIT_TAIL, "full": _lib.SPLIT_FULL,
-               "last": _lib.SPLIT_LAST}
+               "last": _lib.SPLIT_LAST, "stream": _lib.SPLIT_STREAM}
 
 
 def default_waves(block_w, block_t, k_fixed=0):

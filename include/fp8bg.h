@@ -44,7 +44,7 @@ extern "C" {
 
 /* ABI version returned by fp8bg_version(); bumped on any signature or struct
  * change. */
-#define FP8BG_ABI_VERSION 10
+#define FP8BG_ABI_VERSION 11
 
 /* ---- kernel kinds --------------------------------------------------------- */
 /* LDS-tiled kernel: a block_w x block_t workgroup tile, 4 waves in a
@@ -90,6 +90,26 @@ extern "C" {
  * below 2^31 bytes; a launch beyond either limit takes the FP8BG_SPLIT_FULL
  * reduction instead (plan.launches = 2, the same C bit for bit). */
 #define FP8BG_SPLIT_LAST 3
+/* Stream-K (ring kernels with k_fixed 0, waves_k 1 and block_w * block_t
+ * below 256 * 256; config split ignored): for launches with fewer tiles
+ * than CUs.  The tiles x (K/128) units of work are dealt out in equal
+ * contiguous runs, about one per CU (plan.stream_units each: at least half
+ * a tile, less than a whole one, a multiple of `unroll`), so every CU
+ * computes the same number of 128-K groups and a tile is cut between two or
+ * three consecutive runs.  A run that crosses a tile boundary computes the
+ * next tile's head, then the current tile's tail, with one LDS ring running
+ * through both.  The run holding a tile's last group owns it: the other
+ * runs store their fp32 partials (device-scope stores) and count
+ * themselves in the tile's per-wave counters, and the run that finds, or
+ * completes, the full count sums the parts in K order (fixed, so C is the
+ * same bit for bit on every call), writes C and resets the counters.  One
+ * launch; no run waits for another.  Where no tile would be cut (tiles >=
+ * CUs), or the counters (tiles x waves_w x waves_t) exceed FP8BG_COUNTERS,
+ * the launch runs whole tiles instead (plan.stream_units = 0), so the mode
+ * is valid at any M.  The reference's tail split-K role
+ * (kernels/baseline_gluon.py:194-209,274-287), with equal work per CU
+ * instead of whole split tiles. */
+#define FP8BG_SPLIT_STREAM 4
 
 /* Split-K workspace layout (every split mode): FP8BG_COUNTERS uint32 tile
  * counters, then the fp32 partials.  The counters must be zero before a
@@ -135,8 +155,11 @@ typedef struct fp8bg_config {
     int32_t split;      /* cross-workgroup K split factor, in 128-K groups;
                            normalised to 1 when it does not divide K/128
                            (baseline_gluon.py:274-276) */
-    int32_t split_mode; /* FP8BG_SPLIT_* (skinny: NONE, FULL or LAST; tiled
-                           and ring: NONE, TAIL or FULL) */
+    int32_t split_mode; /* FP8BG_SPLIT_* (skinny: NONE, FULL or LAST; tiled:
+                           NONE, TAIL or FULL; ring: NONE, TAIL, FULL, LAST
+                           when block_t <= 64 and k_fixed is 0, STREAM when
+                           k_fixed is 0, waves_k is 1 and block_w * block_t
+                           < 256 * 256) */
     int32_t group_t;    /* tiled: token-tile swizzle group (GROUP_SIZE_M
                            semantics, baseline_triton.py:36-45); >= 1 */
     int32_t flags;      /* FP8BG_FLAG_* */
@@ -165,6 +188,10 @@ typedef struct fp8bg_plan {
     int32_t lds_bytes;  /* LDS used per workgroup */
     int32_t threads;    /* threads per workgroup */
     int32_t kernel_id;  /* index of the compiled kernel instance */
+    int32_t stream_units; /* FP8BG_SPLIT_STREAM: 128-K groups (tile x group
+                           units) per workgroup; 0 when the launch runs whole
+                           tiles.  ws_elems then counts FP8BG_COUNTERS plus
+                           2 * grid * block_w * block_t fp32 partials. */
 } fp8bg_plan;
 
 /* Library ABI version: FP8BG_ABI_VERSION of the build. */
