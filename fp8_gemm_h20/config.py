@@ -59,7 +59,7 @@ def weight_tile(entry):
 
 def _native_ok(impl, c, k):
     """A gfx950-native entry names a compiled kernel instance."""
-    from .kernels import TILED, SKINNY_TILES, RING
+    from .kernels import TILED, SKINNY_TILES, RING, RING_SK
     tw, tt = c.get("BLOCK_W"), c.get("BLOCK_T")
     if c.get("LDS_SWIZZLE", "row16") not in ("row8", "row16", "pair"):
         return False
@@ -68,11 +68,13 @@ def _native_ok(impl, c, k):
         kf = c.get("K_FIXED", 0)
         ku = c.get("K_UNROLL", 1)
         split = c.get("SPLIT", 1) if c.get("SPLIT_MODE", "none") != "none" else 1
-        # SPLIT_MODE "last": the instances with the in-kernel reduction (RING_LAST)
-        modes = _SPLIT_MODES + (("last",) if tt is not None and tt <= 64 and kf == 0 else ())
+        inst = (tw, tt, c.get("WAVES_W"), c.get("WAVES_T"), c.get("STAGES"), kf, ku, c.get("WAVES_K", 1))
+        # SPLIT_MODE "last": the instances with the in-kernel reduction
+        # (RING_LAST); "stream": those with a stream-K kernel (RING_SK)
+        modes = _SPLIT_MODES + (("last",) if tt is not None and tt <= 64 and kf == 0 else ()) + \
+            (("stream",) if inst in RING_SK else ())
         return (c.get("SPLIT_MODE", "none") in modes and (kf == 0 or k == 256 * kf // 2) and
-                (tw, tt, c.get("WAVES_W"), c.get("WAVES_T"), c.get("STAGES"), kf, ku,
-                 c.get("WAVES_K", 1)) in RING and
+                inst in RING and
                 (k // 128 // (split if (k // 128) % split == 0 else 1)) % ku == 0)
     if impl == "skinny":
         mode = c.get("SPLIT_MODE", "none")
