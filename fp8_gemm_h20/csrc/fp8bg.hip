@@ -41,12 +41,19 @@
 //                   (global_load_lds_dwordx4) into an ST-stage LDS ring, one
 //                   barrier per 128-K group, 4 or 8 waves, the next group's
 //                   loads spread over the MFMA stream; C staged through LDS
-//                   and written as whole lines; split-K as fp8bg_tiled.
+//                   and written as whole lines; split-K as fp8bg_tiled, or
+//                   reduced inside the kernel (fp8bg_ring_last), or
+//                   stream-K (fp8bg_ring_sk).
 //  * fp8bg_split_reduce - fixed-order sum of split-K partials -> bf16.
 //  * fp8bg_quant_act_kernel - bf16 activations -> e4m3 + fp32 group scales.
 // Every reduction order is fixed by the configuration, so results are bitwise
-// reproducible run to run and under hipGraph replay.  No kernel uses atomics,
-// fences beyond workgroup scope, or spin waits.
+// reproducible run to run and under hipGraph replay.  The in-kernel
+// reductions (FP8BG_SPLIT_LAST, FP8BG_SPLIT_STREAM) count finished partials
+// with relaxed agent-scope atomics on per-tile counters, after the partials'
+// device-scope (SC1) stores have completed, and read them with device-scope
+// loads; whichever workgroup completes a count sums the partials and resets
+// the counter.  No kernel uses fences beyond workgroup scope or spin waits,
+// and no workgroup waits for another.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -2729,9 +2736,12 @@ int gemm_enqueue(const void* A, const void* B, const float* As, int64_t as_strid
 // process ends.  In host code `scratch` names a host-side stand-in, not a
 // device address; kernels receive the per-device address that
 // hipGetSymbolAddress returns, looked up once per device with that device
-// current and kept in scratch_ptr.  No part of it needs to start at zero:
-// every split workgroup writes its whole fp32 slab before the reduction
-// kernel (later on the same stream) reads it.
+// current and kept in scratch_ptr.  Its layout is the workspace's:
+// FP8BG_COUNTERS tile counters, then the partials.  The counters must start
+// at zero: they do because the array is zero-filled when the code object
+// loads, and every in-kernel reduction (FP8BG_SPLIT_LAST, _STREAM) resets
+// each counter it completes, so every call leaves them zero.  The partials
+// need no clearing: every split call writes each partial it reads.
 static __device__ __align__(256) float scratch[FP8BG_SCRATCH_ELEMS];
 
 constexpr int kMaxDevices = 64;

@@ -18,8 +18,9 @@ Two families of config dicts are accepted:
     ("none", "full" or "last": the split reduced inside the kernel),
     XCD_REMAP (small-M kernel, waves split K);
   - impl "ring": BLOCK_W, BLOCK_T, WAVES_W, WAVES_T, STAGES, K_UNROLL, WAVES_K, SPLIT,
-    SPLIT_MODE, GROUP_SIZE_M, XCD_REMAP, LDS_SWIZZLE (direct-to-LDS ring
-    kernel);
+    SPLIT_MODE ("none", "tail", "full", "last" on token tiles up to 64, or
+    "stream": stream-K), GROUP_SIZE_M, XCD_REMAP, LDS_SWIZZLE (direct-to-LDS
+    ring kernel);
   - impl "shortk": BLOCK_W, BLOCK_T (K == 256, no K loop).
 * the reference's H20 entries (impl "triton", "gluon", "v2", "scale_tma",
   "shortk" with BM/BN keys), translated onto the nearest compiled gfx950 tile

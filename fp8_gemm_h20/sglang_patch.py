@@ -26,6 +26,7 @@ or load the HIP library; both wait for the first patched call.
 import importlib.abc
 import importlib.machinery
 import os
+import warnings
 import sys
 
 TARGET = "sglang.srt.layers.quantization.fp8_utils"
@@ -60,21 +61,42 @@ def eligible(profile, input, weight, block_size, weight_scale, input_scale, bias
             and supports(profile, input.numel() // k, n, k))
 
 
+_OOM_WARNED = []
+
+
 def shuffled_copy(weight):
     """The weight in the shuffled layout, made on its first eligible call
     and kept on the tensor (made again after an in-place change of the
     weight, which bumps its version counter); the row-major weight stays for
     SGLang's own paths.  None while a CUDA graph is being captured: a copy
     made there would live in the graph's memory pool, so a weight first seen
-    during capture runs row-major until an eager call makes its copy."""
+    during capture runs row-major until an eager call makes its copy.
+
+    The copies double the weights' memory (about 35 GB for the 35B model),
+    allocated during SGLang's warm-up, after it has sized its KV-cache pool
+    from the free memory: lower --mem-fraction-static by the weights' share
+    when enabling them.  A copy that does not fit is not made: that weight
+    runs row-major (the same C bit for bit), with one warning per process."""
     import torch
     from . import shuffle_weight
     held = getattr(weight, "_fp8mm_shuffled", None)
     if held is not None and held[0] == weight._version:
         return held[1]
+    if held is not None and held[1] is None:
+        return None                          # no room for this weight's copy
     if torch.cuda.is_current_stream_capturing():
         return None
-    held = (weight._version, shuffle_weight(weight))
+    try:
+        copy = shuffle_weight(weight)
+    except torch.cuda.OutOfMemoryError:
+        if not _OOM_WARNED:
+            _OOM_WARNED.append(True)
+            warnings.warn("fp8mm: no memory for a shuffled weight copy (FP8MM_SHUFFLE_WEIGHTS=1); "
+                          "such weights run row-major.  Lower SGLang's --mem-fraction-static by the "
+                          "FP8 weights' share to make room for the copies.", RuntimeWarning)
+        weight._fp8mm_shuffled = (weight._version, None)
+        return None
+    held = (weight._version, copy)
     weight._fp8mm_shuffled = held
     return held[1]
 

@@ -253,9 +253,13 @@ int fp8bg_gemm(const void* A, const void* B,
  *   - Every call on one GPU shares that GPU's scratch, which keeps the last
  *     split call's partials.  Nothing in it needs clearing: each split call
  *     writes all the partials it reads, and the tile counters of
- *     FP8BG_SPLIT_LAST start at zero (the array is zero when the library
- *     loads) and are left zero by every call.  Split calls that overlap on
- *     one GPU (different streams, or threads without ordering) race on it.
+ *     FP8BG_SPLIT_LAST and FP8BG_SPLIT_STREAM start at zero (the array is
+ *     zero when the library loads) and are left zero by every call.  Split
+ *     calls that overlap on one GPU (different streams, or threads without
+ *     ordering) race on it.
+ *   - Safe to call during hipGraph capture, including a process's first
+ *     call on a device (tested): the call makes no stream-ordered request
+ *     besides its kernel launches, and the graph keeps the scratch address.
  */
 #define FP8BG_SCRATCH_ELEMS (1 << 22)
 int fp8bg_gemm_noalloc(const void* A, const void* B,
