@@ -1562,15 +1562,20 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
     // assignment, so each MFMA still reduces exactly its group's 128 products.
     const int lr = lane >> 2, lc = lane & 3;
     const int op_src = (4 * r + q) << 2;
-    // The Bs block of the whole tile (TW divides 128, so the tile's rows
-    // share one) and the As rows, read with one load per batch: lane l takes
-    // group slot u of token row l >> 2 (row-major As: a quad reads 4 nearby
-    // floats of one row) or u = l >> 4 of row l & 15 (column-major As), and
-    // lane (r, q) gets its row's scale of slot u by ds_bpermute.
-    static_assert(128 % TW == 0, "a skinny tile lies inside one 128-row Bs block");
+    // The Bs block of the whole tile (where TW divides 128 the tile's rows
+    // share one; a 48-row tile may reach into the next block, whose scales
+    // come from a second pointer, and each 16-row block takes the scale of
+    // the block holding its rows) and the As rows, read with one load per
+    // batch: lane l takes group slot u of token row l >> 2 (row-major As: a
+    // quad reads 4 nearby floats of one row) or u = l >> 4 of row l & 15
+    // (column-major As), and lane (r, q) gets its row's scale of slot u by
+    // ds_bpermute.
+    constexpr bool kTwoBs = 128 % TW != 0;
+    static_assert(TW <= 128 && (TW % 16) == 0, "a skinny tile spans at most two 128-row Bs blocks");
     const bool as_cm = a.as_sm == 1;
     const int sa_row = as_cm ? (lane & 15) : lr, sa_u = as_cm ? (lane >> 4) : lc;
     const float* bsp = a.Bs + (int64_t)(w0 >> 7) * a.bs_sn;
+    const float* bsp2 = kTwoBs ? a.Bs + (int64_t)min((w0 + TW - 1) >> 7, a.N / 128 - 1) * a.bs_sn : bsp;
     // shuffled B: block (b, g) of 16 rows and one group at (b K/128 + g) 2 KB
     const int KGB = a.K / kGroupK;
     const uint8_t* wp[NWB];
@@ -1622,7 +1627,7 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
         i32x8 tv[U][NTB];                                       // quantised tokens (QA)
         i32x4 xr[QA ? U : 1][QA ? NTB : 1][QF ? 1 : 4];
         float sa[U][NTB];                                       // token scales (QA)
-        float sar[NTB], sbr;                                    // lane-indexed scales
+        float sar[NTB], sbr, sbr2;                              // lane-indexed scales
     };
     // Loads are issued unconditionally (a group index past the wave's last
     // group is clamped to it; compute skips those), so they form straight-
@@ -1653,6 +1658,7 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
             }
         }
         b.sbr = bsp[(int64_t)group(j0 + min(lane, U - 1)) * a.bs_sk];
+        if constexpr (kTwoBs) b.sbr2 = bsp2[(int64_t)group(j0 + min(lane, U - 1)) * a.bs_sk];
         if (!QA) {
 #pragma unroll
             for (int t = 0; t < NTB; ++t) b.sar[t] = asp[t][(int64_t)group(j0 + min(sa_u, U - 1)) * a.as_sk];
@@ -1794,6 +1800,8 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
         for (int u = 0; u < U; ++u) {
             if (j0 + u < J) {
                 const float sb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b.sbr), u));
+                const float sb2 =
+                    kTwoBs ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b.sbr2), u)) : sb;
                 i32x8 tv[NTB];
                 float sa[NTB];
 #pragma unroll
@@ -1830,17 +1838,20 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                                                    b.wl[u][w][0][3], b.wl[u][w][1][0], b.wl[u][w][1][1],
                                                    b.wl[u][w][1][2], b.wl[u][w][1][3]}
                                          : gather(b.wl[u][w]);
+                    // (wave-uniform: the block of this 16-row block's rows)
+                    const float sbw = kTwoBs && ((w0 + 16 * w) >> 7) != (w0 >> 7) ? sb2 : sb;
 #pragma unroll
-                    for (int t = 0; t < NTB; ++t) promote(acc[w][t], mfma16x16x128(wv, tv[t]), sa[t] * sb);
+                    for (int t = 0; t < NTB; ++t) promote(acc[w][t], mfma16x16x128(wv, tv[t]), sa[t] * sbw);
                 }
             }
         }
     };
     // operand VGPRs of one batch: weights, tokens (and their bf16 source);
     // two batches and the accumulators must leave room for the rest
-    // (16 waves per workgroup leave 128 VGPRs per wave, fewer waves 256)
+    // (16 waves per workgroup leave 128 VGPRs per wave, fewer waves 256;
+    // the 48-row tiles' second Bs scale takes more: 48x64 spills at 160)
     constexpr int kBatchRegs = U * (NWB + NTB + (QF ? 1 : QA ? 2 * NTB : 0)) * 8;
-    constexpr bool kPipe = 2 * kBatchRegs + 4 * NWB * NTB <= (S >= 16 ? 72 : 160);
+    constexpr bool kPipe = 2 * kBatchRegs + 4 * NWB * NTB <= (S >= 16 ? 72 : kTwoBs ? 150 : 160);
     if (J > 0) {
         if constexpr (kPipe) {
             // batches alternate between b0 and b1; the wave's last batch is
@@ -2087,6 +2098,7 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(256, 128, 4, 1, 2)
 
 // skinny: (weight 16-blocks, token 16-blocks, waves splitting K, groups in flight)
+// (the 48-row tiles: N = 12288 in 256 of them, one per CU)
 #define FP8BG_SKINNY(X)                                                        \
     X(1, 1, 4, 1) X(1, 1, 4, 2) X(1, 1, 8, 1) X(1, 1, 8, 2) X(1, 1, 8, 4)      \
     X(2, 1, 4, 1) X(2, 1, 4, 2) X(2, 1, 8, 1) X(2, 1, 8, 2) X(2, 1, 8, 4)      \
@@ -2099,7 +2111,10 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(4, 4, 4, 1) X(4, 4, 8, 1) X(4, 4, 4, 2)                                  \
     X(1, 1, 4, 4) X(2, 1, 4, 4) X(4, 1, 4, 4)                                  \
     X(1, 1, 16, 1) X(1, 1, 16, 2) X(2, 1, 16, 1) X(2, 1, 16, 2) X(4, 1, 16, 1) \
-    X(1, 2, 16, 1) X(2, 2, 16, 1) X(1, 4, 16, 1)
+    X(1, 2, 16, 1) X(2, 2, 16, 1) X(1, 4, 16, 1)                               \
+    X(3, 1, 4, 1) X(3, 1, 4, 2) X(3, 1, 8, 1) X(3, 1, 8, 2)                    \
+    X(3, 2, 4, 2) X(3, 2, 8, 1) X(3, 2, 8, 2)                                  \
+    X(3, 4, 4, 1) X(3, 4, 8, 1) X(3, 4, 4, 2)
 
 // ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 //        K slices)

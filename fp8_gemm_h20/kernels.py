@@ -63,15 +63,20 @@ SKINNY = (
     # dependent memory round trips
     (1, 1, 16, 1), (1, 1, 16, 2), (2, 1, 16, 1), (2, 1, 16, 2), (4, 1, 16, 1),
     (1, 2, 16, 1), (2, 2, 16, 1), (1, 4, 16, 1),
+    # 48 weight rows: N = 12288 in 256 tiles, one per CU (a tile may reach
+    # into a second 128-row Bs block)
+    (3, 1, 4, 1), (3, 1, 4, 2), (3, 1, 8, 1), (3, 1, 8, 2),
+    (3, 2, 4, 2), (3, 2, 8, 1), (3, 2, 8, 2),
+    (3, 4, 4, 1), (3, 4, 8, 1), (3, 4, 4, 2),
 )
 # skinny instances as (block_w, block_t, waves_k, unroll)
 SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
 # skinny with the activation quantiser fused (16-, 32- and 64-token tiles,
-# except those whose bf16 staging would spill); must match FP8BG_SKINNY_QA in
-# csrc/fp8bg.hip
+# except those whose bf16 staging would spill, and the 48-row tiles); must
+# match FP8BG_SKINNY_QA in csrc/fp8bg.hip
 SKINNY_QA = tuple(c for c in SKINNY
                   if c not in ((4, 1, 8, 4), (4, 1, 4, 4), (4, 1, 16, 1), (2, 4, 8, 2), (1, 4, 16, 1))
-                  and c[0] * c[1] <= 8)
+                  and c[0] * c[1] <= 8 and c[0] != 3)
 # ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 #        K slices)
 RING = (
