@@ -72,11 +72,11 @@ SKINNY = (
 # skinny instances as (block_w, block_t, waves_k, unroll)
 SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
 # skinny with the activation quantiser fused (16-, 32- and 64-token tiles,
-# except those whose bf16 staging would spill, and the 48-row tiles); must
-# match FP8BG_SKINNY_QA in csrc/fp8bg.hip
+# except those whose bf16 staging would spill); must match FP8BG_SKINNY_QA in
+# csrc/fp8bg.hip
 SKINNY_QA = tuple(c for c in SKINNY
                   if c not in ((4, 1, 8, 4), (4, 1, 4, 4), (4, 1, 16, 1), (2, 4, 8, 2), (1, 4, 16, 1))
-                  and c[0] * c[1] <= 8 and c[0] != 3)
+                  and c[0] * c[1] <= 8)
 # ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 #        K slices)
 RING = (
