@@ -68,6 +68,7 @@ SKINNY = (
     (3, 1, 4, 1), (3, 1, 4, 2), (3, 1, 8, 1), (3, 1, 8, 2),
     (3, 2, 4, 2), (3, 2, 8, 1), (3, 2, 8, 2),
     (3, 4, 4, 1), (3, 4, 8, 1), (3, 4, 4, 2),
+    (3, 1, 16, 1), (3, 2, 16, 1),
 )
 # skinny instances as (block_w, block_t, waves_k, unroll)
 SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
@@ -75,7 +76,8 @@ SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
 # except those whose bf16 staging would spill); must match FP8BG_SKINNY_QA in
 # csrc/fp8bg.hip
 SKINNY_QA = tuple(c for c in SKINNY
-                  if c not in ((4, 1, 8, 4), (4, 1, 4, 4), (4, 1, 16, 1), (2, 4, 8, 2), (1, 4, 16, 1))
+                  if c not in ((4, 1, 8, 4), (4, 1, 4, 4), (4, 1, 16, 1), (2, 4, 8, 2), (1, 4, 16, 1),
+                               (3, 2, 16, 1))
                   and c[0] * c[1] <= 8)
 # ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 #        K slices)
