@@ -88,11 +88,18 @@ constexpr int kMaxLds = 160 * 1024;   // gfx950 LDS per workgroup
 // B[16 b + (l & 15), 128 g + 64 h + 16 (l >> 4) + e] (l < 64, h < 2, e < 16)
 constexpr int kShufBlock = 16 * kGroupK;
 
+// Bs blocks a ring tile of tw weight rows can span: its first row lies at a
+// multiple of gcd(tw, 128) inside a 128-row block (96-row tiles span two).
+constexpr int ring_bs_blocks(int tw) {
+    int g = 128;
+    while (tw % g) g /= 2;
+    return (128 - g + tw + 127) / 128;
+}
 // Scale-area DMA instructions per wave and stage of the ring kernel: one
 // 64-dword slice per wave carries the tile's As column (tt floats), its Bs
-// blocks (ceil(tw / 128) floats) and the bias row (tw bf16 = tw / 2 dwords).
+// blocks (ring_bs_blocks floats) and the bias row (tw bf16 = tw / 2 dwords).
 constexpr int ring_scale_slices(int tw, int tt, int nwave) {
-    return (tt + (tw + 127) / 128 + tw / 2 + 64 * nwave - 1) / (64 * nwave);
+    return (tt + ring_bs_blocks(tw) + tw / 2 + 64 * nwave - 1) / (64 * nwave);
 }
 constexpr int kNumXcd = 8;            // MI355X: 8 XCDs, workgroups dealt round-robin
 // Word 3 of a gfx9 buffer resource for raw byte-offset loads (no format
@@ -616,7 +623,7 @@ __device__ __forceinline__ void ring_body(const KArgs& a) {
     constexpr int STAGE = OPS + SCALES * 4;
     static_assert(WTW % 16 == 0 && WTT % 16 == 0 && NW >= 1 && NT >= 1, "wave tile");
     static_assert(ROWS % 8 == 0 && NJ >= 1 && NJ * NWAVE - NBLK < NBLK, "DMA blocks per wave");
-    constexpr int NBS = (TW + 127) / 128;         // Bs blocks the tile spans
+    constexpr int NBS = ring_bs_blocks(TW);       // Bs blocks the tile spans
     static_assert(TT + NBS + TW / 2 <= SCALES, "scale slots");
     // epilogue: 16 output rows of a wave at a time, staged in LDS
     constexpr int ROWB = WTW * 2;                 // bf16 bytes of one wave row
@@ -2146,7 +2153,8 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(128, 128, 4, 2, 2, 0, 1, 1) X(128, 128, 4, 2, 3, 0, 1, 1) \
     X(128, 128, 4, 2, 4, 0, 2, 1) X(256, 160, 4, 2, 2, 0, 1, 1) \
     X(256, 192, 4, 2, 2, 0, 1, 1) X(128, 160, 2, 2, 3, 0, 1, 1) \
-    X(128, 96, 2, 2, 4, 0, 1, 1) X(64, 64, 2, 2, 8, 0, 4, 1)
+    X(128, 96, 2, 2, 4, 0, 1, 1) X(64, 64, 2, 2, 8, 0, 4, 1)                   \
+    X(96, 64, 3, 1, 4, 0, 2, 1) X(96, 128, 3, 2, 3, 0, 1, 1)
 #define FP8BG_RING(X) FP8BG_RING_A(X) FP8BG_RING_B(X)
 
 // skinny with the fused activation quantiser: the 16-, 32- and 64-token

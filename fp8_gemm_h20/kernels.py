@@ -112,6 +112,9 @@ RING = (
     (128, 160, 2, 2, 3, 0, 1, 1), (128, 96, 2, 2, 4, 0, 1, 1),
     # 64x64 with 2x2 waves (two weight blocks per wave)
     (64, 64, 2, 2, 8, 0, 4, 1),
+    # 96 weight rows: N = 12288 in 128 tiles, 256 with two token tiles
+    # (a tile may span two 128-row Bs blocks)
+    (96, 64, 3, 1, 4, 0, 2, 1), (96, 128, 3, 2, 3, 0, 1, 1),
 )
 # ring instances with the in-kernel split-K reduction (fp8bg_ring_last,
 # SPLIT_MODE "last"): token tiles up to 64, no fixed K; must match
