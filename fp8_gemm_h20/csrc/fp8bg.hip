@@ -2122,7 +2122,8 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(3, 1, 4, 1) X(3, 1, 4, 2) X(3, 1, 8, 1) X(3, 1, 8, 2)                    \
     X(3, 2, 4, 2) X(3, 2, 8, 1) X(3, 2, 8, 2)                                  \
     X(3, 4, 4, 1) X(3, 4, 8, 1) X(3, 4, 4, 2)                                  \
-    X(3, 1, 16, 1) X(3, 2, 16, 1)
+    X(3, 1, 16, 1) X(3, 2, 16, 1)                                              \
+    X(1, 1, 2, 1) X(2, 1, 2, 1)
 
 // ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 //        K slices)

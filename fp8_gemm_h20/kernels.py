@@ -69,6 +69,8 @@ SKINNY = (
     (3, 2, 4, 2), (3, 2, 8, 1), (3, 2, 8, 2),
     (3, 4, 4, 1), (3, 4, 8, 1), (3, 4, 4, 2),
     (3, 1, 16, 1), (3, 2, 16, 1),
+    # two waves: K = 256 (two 128-K groups) gives each wave one
+    (1, 1, 2, 1), (2, 1, 2, 1),
 )
 # skinny instances as (block_w, block_t, waves_k, unroll)
 SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
@@ -77,7 +79,7 @@ SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
 # csrc/fp8bg.hip
 SKINNY_QA = tuple(c for c in SKINNY
                   if c not in ((4, 1, 8, 4), (4, 1, 4, 4), (4, 1, 16, 1), (2, 4, 8, 2), (1, 4, 16, 1),
-                               (3, 2, 16, 1))
+                               (3, 2, 16, 1), (1, 1, 2, 1), (2, 1, 2, 1))
                   and c[0] * c[1] <= 8)
 # ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 #        K slices)

@@ -52,7 +52,7 @@ extern "C" {
  * Replaces the reference's tiled kernels (kernels/baseline_triton.py:28-81,
  * kernels/baseline_gluon.py:94-211, kernels/kernel_v2.py:94-291). */
 #define FP8BG_KIND_TILED  0
-/* Small-M kernel: no LDS staging; waves_k waves (4, 8 or 16) split the K groups
+/* Small-M kernel: no LDS staging; waves_k waves (2, 4, 8 or 16) split the K groups
  * of one block_w x block_t tile, `unroll` groups in flight per wave, partials
  * summed in fixed wave order.  The reference's SWAP_AB small-M role
  * (kernels/baseline_gluon.py:77-83). */
@@ -145,7 +145,7 @@ typedef struct fp8bg_config {
     int32_t block_t;    /* tokens (M) per workgroup tile */
     int32_t waves_w;    /* tiled/ring: waves along N inside the tile */
     int32_t waves_t;    /* tiled/ring: waves along M inside the tile */
-    int32_t waves_k;    /* skinny: waves splitting K inside a workgroup (4, 8 or 16);
+    int32_t waves_k;    /* skinny: waves splitting K inside a workgroup (2, 4, 8 or 16);
                            ring: K slices of waves_w x waves_t waves (1, 2 or 4;
                            0 means 1) */
     int32_t unroll;     /* skinny: 128-K groups in flight per wave;
