@@ -2175,7 +2175,8 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     X(1, 1, 16, 1) X(1, 1, 16, 2) X(2, 1, 16, 1) X(2, 1, 16, 2)                \
     X(1, 2, 16, 1) X(2, 2, 16, 1)                                              \
     X(3, 1, 4, 1) X(3, 1, 4, 2) X(3, 1, 8, 1) X(3, 1, 8, 2)                    \
-    X(3, 2, 4, 2) X(3, 2, 8, 1) X(3, 2, 8, 2) X(3, 1, 16, 1)
+    X(3, 2, 4, 2) X(3, 2, 8, 1) X(3, 2, 8, 2) X(3, 1, 16, 1)                   \
+    X(1, 1, 2, 1) X(2, 1, 2, 1)
 
 // Launchers, one per compiled instance and B layout; the skinny and ring
 // ones pick the kernel variant at run time.  The arguments travel by pointer

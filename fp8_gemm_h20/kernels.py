@@ -79,7 +79,7 @@ SKINNY_TILES = tuple((16 * w, 16 * t, s, u) for w, t, s, u in SKINNY)
 # csrc/fp8bg.hip
 SKINNY_QA = tuple(c for c in SKINNY
                   if c not in ((4, 1, 8, 4), (4, 1, 4, 4), (4, 1, 16, 1), (2, 4, 8, 2), (1, 4, 16, 1),
-                               (3, 2, 16, 1), (1, 1, 2, 1), (2, 1, 2, 1))
+                               (3, 2, 16, 1))
                   and c[0] * c[1] <= 8)
 # ring: (block_w, block_t, waves_w, waves_t, stages, k_fixed, groups per barrier,
 #        K slices)
