@@ -141,6 +141,7 @@ struct KArgs {
     const uint16_t* X;     // [M, K] bf16, row stride ldx elements
     int64_t ldx;
     float eps;
+    float eps_s, eps_r;    // eps / 448 and 1 / (eps / 448), IEEE fp32 on the host
     uint8_t* q_out;        // optional [M, K] e4m3 copy of the quantised activations
     float* s_out;          // optional [M, K/128] scales, strides qs_sm, qs_sk
     int64_t qs_sm, qs_sk;
@@ -1475,6 +1476,27 @@ void fp8bg_ring_dp_bs(KArgs a) {
     ring_body<TW, TT, WW, WT, ST, KF, KU, WK, true, false, true>(a);
 }
 
+// An activation group's scale s = RN(x / 448) and its reciprocal RN(1 / s),
+// x = max(amax, eps), for the few-token quantiser, where two IEEE division
+// sequences (or a branch around them) would sit on each group's dependent
+// chain.  x is either eps, whose s and 1/s the host computes once, or the
+// bf16 amax itself, at least eps >= 1e-30 > 2^-100.  For a finite bf16 x of
+// at least 2^-100, s is the product with RN(1/448) corrected by one FMA of
+// its exact remainder, and 1/s is v_rcp_f32 (within 1 ulp) refined by one
+// Newton step.  Both equal the correctly rounded quotients there: the
+// quotient was checked for all 32,639 positive finite bf16 x, and the Newton
+// step from every start value within 2 ulp of RN(1/s) for every s of that
+// range (tests/fastdiv_check.c).  From 2^-100 on, no remainder or
+// intermediate is subnormal.
+__device__ __forceinline__ void act_scale_reciprocal_fast(float x, float& s, float& r) {
+#pragma clang fp contract(off)
+    constexpr float kInv448 = 1.0f / 448.0f;
+    const float q0 = x * kInv448;
+    s = __builtin_fmaf(__builtin_fmaf(-q0, 448.0f, x), kInv448, q0);
+    const float r0 = __builtin_amdgcn_rcpf(s);
+    r = __builtin_fmaf(__builtin_fmaf(-s, r0, 1.0f), r0, r0);
+}
+
 // ===========================================================================
 // Small-M kernel: operands straight from global memory, waves split K
 // ===========================================================================
@@ -1713,8 +1735,15 @@ __global__ __launch_bounds__(64 * S) void fp8bg_skinny(KArgs a) {
                     mx = max(mx, (uint32_t)__builtin_amdgcn_mov_dpp((int)mx, 0x124, 0xf, 0xf, false));
                     mx = max(mx, (uint32_t)__builtin_amdgcn_mov_dpp((int)mx, 0x128, 0xf, 0xf, false));
                     const bool nan = mx > 0x7f80u;
-                    const float sc = nan ? __builtin_nanf("") : fmaxf(__uint_as_float(mx << 16), a.eps) / 448.0f;
-                    const float rcp = 1.0f / sc;
+                    // s = max(amax, eps) / 448 and 1/s without a division:
+                    // eps's pair from the host, an infinite amax gives
+                    // (inf, 0), any other amax >= eps the exact fast pair
+                    const float amax = __uint_as_float(mx << 16);
+                    float sf, rf;
+                    act_scale_reciprocal_fast(amax, sf, rf);
+                    const bool inf = mx == 0x7f80u, above = amax >= a.eps;
+                    const float sc = nan ? __builtin_nanf("") : inf ? amax : above ? sf : a.eps_s;
+                    const float rcp = nan ? __builtin_nanf("") : inf ? 0.0f : above ? rf : a.eps_r;
                     int o[2];
 #pragma unroll
                     for (int i = 0; i < 2; ++i) {
@@ -2879,6 +2908,8 @@ int fp8bg_gemm_bf16a(const void* X, int64_t x_stride_m, float eps, const void* B
     a.X = (const uint16_t*)X;
     a.ldx = x_stride_m;
     a.eps = eps;
+    a.eps_s = eps / 448.0f;
+    a.eps_r = 1.0f / a.eps_s;
     a.q_out = (uint8_t*)q_out;
     a.s_out = s_out;
     a.qs_sm = s_stride_m;
