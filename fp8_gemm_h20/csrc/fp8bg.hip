@@ -1477,10 +1477,12 @@ void fp8bg_ring_dp_bs(KArgs a) {
 }
 
 // An activation group's scale s = RN(x / 448) and its reciprocal RN(1 / s),
-// x = max(amax, eps), for the few-token quantiser, where two IEEE division
-// sequences (or a branch around them) would sit on each group's dependent
-// chain.  x is either eps, whose s and 1/s the host computes once, or the
-// bf16 amax itself, at least eps >= 1e-30 > 2^-100.  For a finite bf16 x of
+// x = max(amax, eps), for the activation quantisers: in the few-token one
+// two IEEE division sequences (or a branch around them) would sit on each
+// group's dependent chain, in the standalone one they cost VALU time.  x is
+// either eps, whose s and 1/s the host computes once, or the bf16 amax
+// itself (in the fused kernel at least eps >= 1e-30 > 2^-100; the standalone
+// one takes this pair only where s >= 2^-60).  For a finite bf16 x of
 // at least 2^-100, s is the product with RN(1/448) corrected by one FMA of
 // its exact remainder, and 1/s is v_rcp_f32 (within 1 ulp) refined by one
 // Newton step.  Both equal the correctly rounded quotients there: the
@@ -2076,7 +2078,25 @@ struct QArgs {
     int64_t ldx, s_sm, s_sk;
     int M, K;
     float eps;
+    float eps_s, eps_r;    // eps / 448 and 1 / (eps / 448), IEEE fp32 on the host
 };
+
+// v / s for a bf16 value v and a scale s >= 2^-60 (or +inf), given
+// r = RN(1 / s): the product corrected by one FMA of its exact remainder.
+// It equals the IEEE quotient for every bf16 mantissa against every fp32
+// scale mantissa (tests/divscale_check.c, all 2^31 pairs of one binade
+// each).  Powers of two scale every step exactly wherever the quotient can
+// round to a nonzero e4m3 code (|v / s| >= 2^-11 with s >= 2^-60 keeps v,
+// the product and the remainder's granularity in the normal range); smaller
+// quotients give a signed zero code either way.  An infinite s takes v * 0
+// (+-0, or NaN for an infinite v, as the division gives), and the sign is
+// v's (-0 / s is -0).
+__device__ __forceinline__ float div_by_scale(float v, float s, float r) {
+#pragma clang fp contract(off)
+    const float q0 = v * r;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, s, v), r, q0);
+    return s == __builtin_inff() ? q0 : __builtin_copysignf(q1, v);
+}
 
 // 16 lanes per 128-element group, 8 elements (16 bytes) per lane.
 __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
@@ -2093,26 +2113,46 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
         v[2 * i] = __uint_as_float((uint32_t)raw[i] << 16);
         v[2 * i + 1] = __uint_as_float((uint32_t)raw[i] & 0xffff0000u);
     }
-    // amax with NaN propagation (a NaN anywhere in the group makes its scale
-    // NaN, as max/clamp do in the reference recipe)
-    float amax = 0.f;
-    bool nan = false;
+    // amax as an unsigned max of the bf16 magnitude bits over the group's 16
+    // lanes (exact; a NaN's bits exceed infinity's, so a NaN anywhere makes
+    // the group's scale NaN, as max/clamp do in the reference recipe)
+    uint32_t mx = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        amax = fmaxf(amax, fabsf(v[i]));
-        nan |= __builtin_isnan(v[i]);
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t d = (uint32_t)raw[i] & 0x7fff7fffu;
+        mx = max(mx, max(d & 0xffffu, d >> 16));
     }
 #pragma unroll
-    for (int d = 1; d < 16; d <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, d, 16));
-        nan |= __shfl_xor((int)nan, d, 16) != 0;
-    }
-    const float scale = nan ? __builtin_nanf("") : fmaxf(amax, a.eps) / 448.0f;
+    for (int d = 1; d < 16; d <<= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, d, 16));
+    const bool nan = mx > 0x7f80u, inf = mx == 0x7f80u;
+    const float amax = __uint_as_float(mx << 16);
+    // The scale and its reciprocal without a division (the bf16 amax's exact
+    // pair, eps's pair from the host, (inf, 0) for an infinite amax), and
+    // each value's quotient without one, where every lane's scale is at
+    // least 2^-60 (NaN fails the compare); otherwise the divisions.
+    float sf, rf;
+    act_scale_reciprocal_fast(amax, sf, rf);
+    const bool above = amax >= a.eps;
+    const float scale_f = nan ? __builtin_nanf("") : inf ? amax : above ? sf : a.eps_s;
+    float scale;
     uint2 o;
-    o.x = e4m3_from_f32(v[0] / scale) | (e4m3_from_f32(v[1] / scale) << 8) |
-          (e4m3_from_f32(v[2] / scale) << 16) | (e4m3_from_f32(v[3] / scale) << 24);
-    o.y = e4m3_from_f32(v[4] / scale) | (e4m3_from_f32(v[5] / scale) << 8) |
-          (e4m3_from_f32(v[6] / scale) << 16) | (e4m3_from_f32(v[7] / scale) << 24);
+    if (__builtin_amdgcn_ballot_w64(!(scale_f >= 0x1p-60f)) == 0) {
+        scale = scale_f;
+        const float rs = inf ? 0.0f : above ? rf : a.eps_r;
+        float qv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qv[i] = div_by_scale(v[i], scale, rs);
+        o.x = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+            qv[2], qv[3], __builtin_amdgcn_cvt_pk_fp8_f32(qv[0], qv[1], 0, false), true);
+        o.y = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+            qv[6], qv[7], __builtin_amdgcn_cvt_pk_fp8_f32(qv[4], qv[5], 0, false), true);
+    } else {
+        scale = nan ? __builtin_nanf("") : fmaxf(amax, a.eps) / 448.0f;
+        o.x = e4m3_from_f32(v[0] / scale) | (e4m3_from_f32(v[1] / scale) << 8) |
+              (e4m3_from_f32(v[2] / scale) << 16) | (e4m3_from_f32(v[3] / scale) << 24);
+        o.y = e4m3_from_f32(v[4] / scale) | (e4m3_from_f32(v[5] / scale) << 8) |
+              (e4m3_from_f32(v[6] / scale) << 16) | (e4m3_from_f32(v[7] / scale) << 24);
+    }
     *(uint2*)(a.q + (int64_t)m * a.K + col) = o;
     if (sub == 0) a.s[m * a.s_sm + g * a.s_sk] = scale;
 }
@@ -2947,6 +2987,8 @@ int fp8bg_quant_act(const void* x, int64_t x_stride_m, void* q, float* s, int64_
     a.M = M;
     a.K = K;
     a.eps = eps;
+    a.eps_s = eps / 448.0f;
+    a.eps_r = 1.0f / a.eps_s;
     hipLaunchKernelGGL(fp8bg_quant_act_kernel, dim3((unsigned)blocks), dim3(kThreads), 0,
                        (hipStream_t)stream, a);
     return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
