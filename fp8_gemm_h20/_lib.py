@@ -11,7 +11,7 @@ from pathlib import Path
 
 LIB_NAME = "libfp8bg.so"
 LIB_PATH = Path(__file__).resolve().with_name(LIB_NAME)
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 OK = 0
 ERR_SHAPE = 1
@@ -57,6 +57,7 @@ EXPORTS = (
     "fp8bg_quant_act",
     "fp8bg_shuffle_b",
     "fp8bg_e4m3_encode_host",
+    "fp8bg_e4m3_encode_device",
     "fp8bg_calib_mfma",
     "fp8bg_calib_mfma_promoted",
     "fp8bg_calib_read",
@@ -156,6 +157,8 @@ def _declare(lib):
     lib.fp8bg_shuffle_b.restype = ctypes.c_int
     lib.fp8bg_e4m3_encode_host.argtypes = [vp, vp, i64]
     lib.fp8bg_e4m3_encode_host.restype = ctypes.c_int
+    lib.fp8bg_e4m3_encode_device.argtypes = [vp, vp, i64, vp]
+    lib.fp8bg_e4m3_encode_device.restype = ctypes.c_int
     lib.fp8bg_calib_mfma.argtypes = [vp, vp, i32, i32, vp]
     lib.fp8bg_calib_mfma.restype = ctypes.c_int
     lib.fp8bg_calib_mfma_promoted.argtypes = [vp, vp, vp, i32, i32, vp]

@@ -2157,6 +2157,19 @@ __global__ __launch_bounds__(kThreads) void fp8bg_quant_act_kernel(QArgs a) {
     if (sub == 0) a.s[m * a.s_sm + g * a.s_sk] = scale;
 }
 
+// fp32 -> e4m3 with the instruction the quantisers use (v_cvt_pk_fp8_f32),
+// two values per lane, grid-stride (fp8bg_e4m3_encode_device).
+__global__ __launch_bounds__(kThreads) void fp8bg_e4m3_cvt_kernel(const float* x, uint8_t* out, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; 2 * p < n; p += stride) {
+        const int64_t i = 2 * p;
+        const bool pair = i + 1 < n;
+        const uint32_t d = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[i], pair ? x[i + 1] : 0.0f, 0, false);
+        out[i] = (uint8_t)d;
+        if (pair) out[i + 1] = (uint8_t)(d >> 8);
+    }
+}
+
 #endif  // FP8BG_HOST_PART
 
 // ---------------------------------------------------------------------------
@@ -3065,6 +3078,16 @@ int fp8bg_e4m3_encode_host(const float* x, uint8_t* out, int64_t n) {
     if (!x || !out || n < 0) return FP8BG_ERR_NULL;
     for (int64_t i = 0; i < n; ++i) out[i] = (uint8_t)e4m3_from_f32(x[i]);
     return FP8BG_OK;
+}
+
+int fp8bg_e4m3_encode_device(const float* x, uint8_t* out, int64_t n, void* stream) {
+    if (!x || !out) return FP8BG_ERR_NULL;
+    if (n < 0) return FP8BG_ERR_SHAPE;
+    if (n == 0) return FP8BG_OK;
+    const int64_t blocks = std::min<int64_t>(((n + 1) / 2 + kThreads - 1) / kThreads, 65536);
+    hipLaunchKernelGGL(fp8bg_e4m3_cvt_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, (hipStream_t)stream, x,
+                       out, n);
+    return hipGetLastError() == hipSuccess ? FP8BG_OK : FP8BG_ERR_LAUNCH;
 }
 
 }  // extern "C"

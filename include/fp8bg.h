@@ -44,7 +44,7 @@ extern "C" {
 
 /* ABI version returned by fp8bg_version(); bumped on any signature or struct
  * change. */
-#define FP8BG_ABI_VERSION 11
+#define FP8BG_ABI_VERSION 12
 
 /* ---- kernel kinds --------------------------------------------------------- */
 /* LDS-tiled kernel: a block_w x block_t workgroup tile, 4 waves in a
@@ -335,6 +335,15 @@ int fp8bg_shuffle_b(const void* B, int64_t b_stride_n, void* Bt, int32_t N, int3
  * No reference counterpart (the reference relies on torch's cast).
  */
 int fp8bg_e4m3_encode_host(const float* x, uint8_t* out, int64_t n);
+
+/*
+ * The same conversion on the device, done the way both activation
+ * quantisers do it: the v_cvt_pk_fp8_f32 instruction (two values per lane)
+ * over n floats in device memory; stream-ordered, no sync.  For tests that
+ * pin that instruction against fp8bg_e4m3_encode_host.  No reference
+ * counterpart.
+ */
+int fp8bg_e4m3_encode_device(const float* x, uint8_t* out, int64_t n, void* stream);
 
 /*
  * Calibration kernels: what this chip sustains, measured next to the
