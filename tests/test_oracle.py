@@ -147,6 +147,38 @@ def test_row_independence():
     assert np.allclose(C5[0], C[5], rtol=0, atol=1e-6 * np.abs(C).max())
 
 
+def test_sampled_oracle_block_equals_the_full_product_there():
+    # the GPU tests check a sampled block of a product too large for the
+    # oracle; the block's weight rows take their own block scales
+    from tests import oracle_sample as osm
+    A, B, As, Bs = _rand_case(300, 640, 256, seed=21)
+    rows, cols = osm.spread(300, 40), osm.spread(640, 48)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x))
+    got = osm.oracle_block(t(A).view(torch.float8_e4m3fn), t(B).view(torch.float8_e4m3fn), t(As), t(Bs),
+                           rows, cols)
+    full = ob.dequant_matmul(A, B, As, Bs)[rows][:, cols]
+    assert np.abs(got - full).max() <= 1e-6 * np.abs(full).max()
+    # operands bitwise: the per-row-group dequantiser with Bs[col // 128]
+    # is the block dequantiser on those rows
+    assert np.array_equal(ob.dequant_a(B[cols], Bs[cols // 128]), ob.dequant_b(B, Bs)[cols])
+    # a wrong block scale index (col // 64) is caught
+    assert not np.array_equal(ob.dequant_a(B[cols], Bs[np.minimum(cols // 64, len(Bs) - 1)]),
+                              ob.dequant_b(B, Bs)[cols])
+
+
+def test_sample_spread_covers_every_tile():
+    from tests import oracle_sample as osm
+    for n in (1, 16, 80, 85, 777, 4097, 16384):
+        s = osm.spread(n, osm.ROWS)
+        assert s[0] == 0 and s[-1] == n - 1 and np.all(np.diff(s) > 0)
+        assert len(s) == min(n, osm.ROWS) or (n > osm.ROWS and len(s) <= osm.ROWS)
+        assert set(range(min(n, 8))) <= set(s.tolist())
+        assert len(set((s // 256).tolist())) == (n + 255) // 256
+    for n in (512, 2048, 12288):
+        c = osm.spread(n, osm.COLS)
+        assert len(set((c // 128).tolist())) == n // 128
+
+
 def test_nonsquare_shapes_reject_transposed_operand():
     # A wrong orientation (B instead of B^T, or scale index n//128 vs n) cannot
     # satisfy brute force on a non-square, multi-block case.
