@@ -201,10 +201,40 @@ def _log_nearest(table, m):
     return min(table, key=lambda a: abs(math.log(int(a) / m)))
 
 
+def _split_fits(entry, m, anchor):
+    """Whether a row-split entry (gfx950 extension: rows [M_SPLIT, M) run on
+    TAIL) is used at M: its TAIL was chosen for the anchor's tail rows, so it
+    takes tails up to that many rows rounded up to its own token tile; past
+    that (M routed from far off the anchor), the entry runs whole on its own
+    tile, as a fallback entry does."""
+    c = entry["config"]
+    tt = token_tile(c["TAIL"])
+    return m - c["M_SPLIT"] <= -(-(anchor - c["M_SPLIT"]) // tt) * tt
+
+
+def _routed(entry, m, anchor):
+    """The entry as it runs at M when routed from `anchor`.  Two gfx950
+    structures are fitted to the anchor's own tile count and run only where
+    they still fit, elsewhere the entry's plain tile runs: a row split
+    (_split_fits), and a tail split of the last, partial wave of tiles
+    (SPLIT_MODE "tail"), kept only at M with the anchor's number of token-tile
+    rows (routed further, its leftover tiles and their split-K workspace grow
+    with M)."""
+    c = entry["config"]
+    if "M_SPLIT" in c and not _split_fits(entry, m, anchor):
+        return dict(entry, config={key: v for key, v in c.items() if key not in ("M_SPLIT", "TAIL")})
+    if (entry["impl"] in NATIVE and c.get("SPLIT_MODE") == "tail" and c.get("SPLIT", 1) > 1
+            and -(-m // c["BLOCK_T"]) != -(-anchor // c["BLOCK_T"])):
+        return dict(entry, config={key: v for key, v in c.items() if key not in ("SPLIT", "SPLIT_MODE")})
+    return entry
+
+
 def select_in(data, m, n, k):
     """Policy of config.py:76-101 applied to a validated table dict.
 
-    Returns (entry, {"method": ..., "anchor": int}) without copying.
+    Returns (entry, {"method": ..., "anchor": int}), the table's own entry
+    (not a copy) except where a row split or tail split fitted to the anchor
+    does not fit M, which comes without it (_routed).
     """
     if not supports_in(data, m, n, k):
         raise ValueError(f"{data.get('profile', 'profile')} does not cover M,N,K={m},{n},{k}")
@@ -227,13 +257,13 @@ def select_in(data, m, n, k):
             if best is None or rank < best[0]:
                 best = (rank, anchor, entry)
         if best is not None:
-            return best[2], {"method": "equal_tile_count", "anchor": best[1]}
+            return _routed(best[2], m, best[1]), {"method": "equal_tile_count", "anchor": best[1]}
         table = data["fallback_entries"][nk]
         method = "baseline_fallback"
     else:
         method = "log_nearest"
     anchor = _log_nearest(table, m)
-    return table[anchor], {"method": method, "anchor": int(anchor)}
+    return _routed(table[anchor], m, int(anchor)), {"method": method, "anchor": int(anchor)}
 
 
 def select_fused_in(data, m, n, k):
