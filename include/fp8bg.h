@@ -242,8 +242,8 @@ int fp8bg_gemm(const void* A, const void* B,
  * device memory (code under hipGraph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  No counterpart in the reference.  Same kernels,
  * plan and results as fp8bg_gemm (bitwise), with the split-K partials in a
- * static per-GPU scratch array of FP8BG_SCRATCH_ELEMS fp32 (16 MiB; no
- * entry of the packaged gfx950 tables splits K at present).  Calls
+ * static per-GPU scratch array of FP8BG_SCRATCH_ELEMS fp32 (16 MiB; every
+ * entry of the packaged gfx950 tables fits it, where it is routed).  Calls
  * nothing that allocates: no hipMalloc/hipFree, no library allocator.
  *   - A launch whose plan needs more than FP8BG_SCRATCH_ELEMS workspace
  *     elements returns FP8BG_ERR_SCRATCH before anything is enqueued.
